@@ -1,0 +1,120 @@
+/*
+ * popcorn_amd C ABI: hand-written gfx950 (MI355X) kernels for Popcorn's
+ * transformer-block ops, reached from Python through ctypes.
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer is a device pointer owned by the caller (torch);
+ *   - sizes and strides are int64, strides count elements, the last dimension
+ *     is always contiguous;
+ *   - `stream` is a hipStream_t; work is enqueued there and nothing synchronises;
+ *   - the return value is a PK_* status; on anything but PK_OK the reason is in
+ *     pk_last_error() (a per-thread string). No entry point falls back to
+ *     another implementation: an unsupported call is an error.
+ *
+ * Popcorn has no C ABI of its own (its implementations are Python callables
+ * registered with `op.register(name, source=...)`, core/dispatcher.py:324-345).
+ * Each entry point below names the Popcorn reference whose arithmetic it
+ * replaces and the first-party implementation it stands beside.
+ */
+#ifndef POPCORN_AMD_H
+#define POPCORN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_ABI_VERSION 1
+
+/* status codes */
+#define PK_OK 0
+#define PK_ERR_INVALID 1     /* bad argument: null pointer, negative size, misalignment */
+#define PK_ERR_UNSUPPORTED 2 /* valid call outside what the kernels implement */
+#define PK_ERR_HIP 3         /* the HIP runtime refused a launch */
+
+/* element types */
+#define PK_F32 0
+#define PK_BF16 1
+#define PK_F16 2
+
+/* ABI version of the loaded library (PK_ABI_VERSION at build time). */
+int pk_version(void);
+
+/* Message of the last failing call on this thread ("" after a success). */
+const char* pk_last_error(void);
+
+/*
+ * SwiGLU forward, y = silu(a) * b over n elements, all of dtype `dtype`.
+ * Rounding follows torch eager: silu is rounded to `dtype`, then the product.
+ * Replaces: reference `swiglu` (kernels/swiglu.py:9-18, `F.silu(a) * b`);
+ * stands beside the CUDA `fwd` host function (impls/swiglu.cu:77-101).
+ */
+int pk_swiglu_fwd(const void* a, const void* b, void* y, int64_t n, int dtype, void* stream);
+
+/*
+ * SwiGLU backward: s = sigmoid(a); da = dy*b*s*(1 + a*(1-s)); db = dy*a*s,
+ * computed in fp32 and rounded once. Replaces torch autograd of the reference
+ * (kernels/swiglu.py:18); stands beside `bwd` (impls/swiglu.cu:103-130).
+ */
+int pk_swiglu_bwd(const void* dy, const void* a, const void* b, void* da, void* db, int64_t n, int dtype,
+                  void* stream);
+
+/*
+ * RMSNorm forward over `rows` contiguous rows of `cols` elements:
+ *   r = 1/sqrt(mean(x^2) + eps); y = round(round(x*r) * w) [+ bias].
+ * x, w, bias and y share `dtype`; bias may be NULL; rstd (fp32 [rows]) may be
+ * NULL and otherwise receives r for the backward pass.
+ * Replaces: reference `rms_norm` (kernels/rms_norm.py:16-30) with `rms`
+ * (kernels/_utils.py:14-16).
+ */
+int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, float* rstd, int64_t rows, int64_t cols,
+                   float eps, int dtype, void* stream);
+
+/* Bytes of device workspace pk_rmsnorm_bwd needs for this shape. */
+int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
+
+/*
+ * RMSNorm backward. With n = x*r and u = dy*w:
+ *   dx = r*(u - n*mean(u*n)), dw = sum_rows dy*n, dbias = sum_rows dy.
+ * Accumulation is fp32 and deterministic (per-block partial rows in
+ * `workspace`, then one column reduction); dw and dbias are rounded once to
+ * `dtype`. dbias may be NULL. rstd is the forward's output.
+ * Replaces torch autograd of the reference (kernels/rms_norm.py:29-30).
+ */
+int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
+                   void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream);
+
+/*
+ * Rotary embedding of x [batch, seq, heads, head_dim] with tables
+ * cos, sin [seq, half] (contiguous), in fp32 arithmetic, rounded once to x's
+ * dtype. NeoX halves (interleaved = 0): pairs (j, j + half); GPT-J
+ * (interleaved = 1): pairs (2j, 2j + 1). Channels from 2*half on are copied.
+ * conjugate = 1 negates sin (the backward rotation). y may equal x (in place).
+ * strides[6] = x (batch, seq, head) strides then y's, in elements.
+ * Replaces: reference `rotary_embedding` (kernels/rotary_embedding.py:12-40);
+ * stands beside the Triton `_rotary_kernel` (impls/rotary_embedding_tl.py:17-67).
+ */
+int pk_rotary(const void* x, const void* cos, const void* sin, void* y, const int64_t* strides, int64_t batch,
+              int64_t seq, int64_t heads, int64_t head_dim, int64_t half, int x_dtype, int cs_dtype, int interleaved,
+              int conjugate, void* stream);
+
+/*
+ * Attention forward, o = softmax(q k^T * scale + M) v, grouped-query:
+ * q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim],
+ * o like q; q head h reads kv head h / (q_heads / kv_heads). causal = 1 masks
+ * key j > query i (top-left aligned). lse (fp32 [batch, q_heads, seq],
+ * natural log) may be NULL. strides[12] = q, k, v, o (batch, seq, head)
+ * strides in elements. dtype is PK_BF16 or PK_F16; head_dim 64 or 128.
+ * Replaces: reference `attn` (kernels/attn.py:10-37,
+ * F.scaled_dot_product_attention with enable_gqa=True).
+ */
+int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int64_t* strides,
+                int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
+                int causal, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POPCORN_AMD_H */

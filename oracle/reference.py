@@ -1,0 +1,183 @@
+"""CPU oracle: float64 numpy restatement of Popcorn's transformer-block references.
+
+TEST INFRASTRUCTURE ONLY. Only `tests/`, `__graft_entry__.smoke()` and the
+`cpu_baseline` leg of `bench.py` may import this module, and only as the
+checker / the CPU figure. The product path (`popcorn_amd`) never calls it.
+
+Every function restates the arithmetic of one Popcorn reference (cited
+file:line under tilde-research/popcorn) in float64, with no rounding between
+steps: this is the "truth" of Popcorn's comparison rule (bench/compare.py:205,
+the reference evaluated on float64 clones), which removes every intermediate
+cast. The forward formulas are Popcorn's; the backward formulas are the
+closed-form derivatives of those forwards (Popcorn takes them from torch
+autograd, bench/compare.py:243-278).
+
+Pinning (tests/test_oracle.py): every function is checked against at least one
+independent fact that a plausible slip would break:
+  rms_norm          torch.nn.functional.rms_norm (float64); output RMS closed form;
+                    scale invariance; zero row -> 0
+  rms_norm_bwd      float64 autograd of F.rms_norm; central finite differences;
+                    <dx, x> = 0 when w = 1, eps = 0; dw = sum dy*n
+  swiglu            scipy.special.expit formulation; silu(0) = 0; silu(x) -> x
+  swiglu_bwd        central finite differences; float64 autograd of F.silu
+  rotary_embedding  complex multiplication (x1 + i x2)(c + i s); identity tables;
+                    norm preservation for unit tables; conjugate inverts forward
+  attention         explicit per-query loops; float64 SDPA with repeat_interleave;
+                    q = 0 gives prefix means of v and lse = log(t + 1); S = 1 gives v
+No function here is "parity unpinned".
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "rms_norm",
+    "rms_norm_bwd",
+    "swiglu",
+    "swiglu_bwd",
+    "rotary_embedding",
+    "rotary_embedding_bwd",
+    "attention",
+    "attention_rows",
+]
+
+
+def _f64(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float64)
+
+
+def rms_norm(x, weight, bias=None, eps: float = 1e-6) -> np.ndarray:
+    """y = x * rsqrt(mean(x^2, -1) + eps) * weight (+ bias).
+
+    Follows kernels/rms_norm.py:29-30 and `rms` kernels/_utils.py:14-16
+    (mean over the last axis, eps inside the square root).
+    """
+    x, w = _f64(x), _f64(weight)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    y = x * r * w
+    return y if bias is None else y + _f64(bias)
+
+
+def rms_norm_bwd(x, weight, dy, eps: float = 1e-6):
+    """Gradients of `rms_norm` for cotangent dy: (dx, dweight, dbias).
+
+    With r = (mean(x^2) + eps)^-1/2, n = x r, u = dy w:
+      dx = r (u - n mean(u n)),  dweight = sum_rows dy n,  dbias = sum_rows dy.
+    """
+    x, w, g = _f64(x), _f64(weight), _f64(dy)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    n = x * r
+    u = g * w
+    dx = r * (u - n * np.mean(u * n, axis=-1, keepdims=True))
+    lead = tuple(range(x.ndim - 1))
+    return dx, np.sum(g * n, axis=lead), np.sum(g, axis=lead)
+
+
+def _sigmoid(a: np.ndarray) -> np.ndarray:
+    # split by sign so exp never overflows
+    out = np.empty_like(a)
+    pos = a >= 0
+    out[pos] = 1.0 / (1.0 + np.exp(-a[pos]))
+    e = np.exp(a[~pos])
+    out[~pos] = e / (1.0 + e)
+    return out
+
+
+def swiglu(a, b) -> np.ndarray:
+    """y = silu(a) * b, silu(a) = a * sigmoid(a). kernels/swiglu.py:18."""
+    a, b = _f64(a), _f64(b)
+    return a * _sigmoid(a) * b
+
+
+def swiglu_bwd(dy, a, b):
+    """(da, db) of `swiglu`: s = sigmoid(a); da = dy b s (1 + a (1 - s)); db = dy a s.
+
+    The same closed form as impls/swiglu.cu:60-61.
+    """
+    g, a, b = _f64(dy), _f64(a), _f64(b)
+    s = _sigmoid(a)
+    return g * b * s * (1.0 + a * (1.0 - s)), g * a * s
+
+
+def rotary_embedding(x, cos, sin, interleaved: bool = False) -> np.ndarray:
+    """Rotate channel pairs of x [batch, seq, heads, head_dim] by cos/sin [seq, half].
+
+    kernels/rotary_embedding.py:35-46: NeoX pairs (j, j + half) or GPT-J
+    pairs (2j, 2j + 1); y1 = x1 c - x2 s, y2 = x1 s + x2 c; channels from
+    2*half on are copied unchanged.
+    """
+    x = _f64(x)
+    c = _f64(cos)[None, :, None, :]
+    s = _f64(sin)[None, :, None, :]
+    half = c.shape[-1]
+    y = x.copy()
+    if interleaved:
+        x1, x2 = x[..., 0 : 2 * half : 2], x[..., 1 : 2 * half : 2]
+        y[..., 0 : 2 * half : 2] = x1 * c - x2 * s
+        y[..., 1 : 2 * half : 2] = x1 * s + x2 * c
+    else:
+        x1, x2 = x[..., :half], x[..., half : 2 * half]
+        y[..., :half] = x1 * c - x2 * s
+        y[..., half : 2 * half] = x1 * s + x2 * c
+    return y
+
+
+def rotary_embedding_bwd(dy, cos, sin, interleaved: bool = False) -> np.ndarray:
+    """dx of `rotary_embedding`: the transpose of the rotation, i.e. rotation by -sin."""
+    return rotary_embedding(dy, cos, -_f64(sin), interleaved)
+
+
+def attention_rows(q, k, v, rows, causal: bool, scale: float | None = None):
+    """o and lse for selected query rows of one (batch, head): q [S, D], k, v [S, D].
+
+    softmax(q k^T scale + M) v as in kernels/attn.py:30-37 (SDPA, top-left
+    causal mask: key j visible to query i iff j <= i). lse = log sum exp of the
+    masked scaled scores (natural log). Returns (o [len(rows), D], lse [len(rows)]).
+    """
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    d = q.shape[-1]
+    scale = d**-0.5 if scale is None else scale
+    rows = np.asarray(rows)
+    out = np.empty((rows.size, v.shape[-1]))
+    lse = np.empty(rows.size)
+    for n, i in enumerate(rows):
+        keys = k[: i + 1] if causal else k
+        vals = v[: i + 1] if causal else v
+        s = keys @ q[i] * scale
+        m = s.max()
+        p = np.exp(s - m)
+        total = p.sum()
+        out[n] = p @ vals / total
+        lse[n] = m + np.log(total)
+    return out, lse
+
+
+def attention(q, k, v, causal: bool = False, scale: float | None = None):
+    """Grouped-query attention over q [B, S, Hq, D], k, v [B, S, Hkv, D].
+
+    q head h reads kv head h // (Hq / Hkv) (SDPA's enable_gqa grouping,
+    kernels/attn.py:30-37). Returns (o [B, S, Hq, D], lse [B, Hq, S]).
+    """
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    batch, seq, hq, d = q.shape
+    hkv = k.shape[2]
+    if hq % hkv:
+        raise ValueError("q heads must be a multiple of kv heads")
+    group = hq // hkv
+    scale = d**-0.5 if scale is None else scale
+    o = np.empty_like(q)
+    lse = np.empty((batch, hq, seq))
+    mask = np.triu(np.ones((seq, seq), dtype=bool), 1) if causal else None
+    for b in range(batch):
+        for h in range(hq):
+            kh, vh = k[b, :, h // group], v[b, :, h // group]
+            s = q[b, :, h] @ kh.T * scale
+            if mask is not None:
+                s = np.where(mask, -np.inf, s)
+            m = s.max(axis=-1, keepdims=True)
+            p = np.exp(s - m)
+            total = p.sum(axis=-1, keepdims=True)
+            o[b, :, h] = p @ vh / total
+            lse[b, h] = (m + np.log(total))[:, 0]
+    return o, lse

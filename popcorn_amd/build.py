@@ -1,0 +1,80 @@
+"""Build recipe for the HIP kernel library: hipcc for gfx950, in-tree output.
+
+`python -m popcorn_amd.build` compiles every `csrc/*.hip` to an object in
+`popcorn_amd/_build/` (in parallel) and links `popcorn_amd/libpopcorn_amd.so`.
+The library is always rebuilt: the call is the "does it build" check.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+BUILD = PACKAGE / "_build"
+LIBRARY = PACKAGE / "libpopcorn_amd.so"
+INCLUDE = PACKAGE.parent / "include"
+
+ARCH = "gfx950"
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # The kernels reproduce torch's rounding sequence (separate products and
+    # sums); contraction would fuse them. FMAs are written out where wanted.
+    "-ffp-contract=off",
+    # Packed fp32 VALU ops are kept out of every kernel.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+]
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found; the popcorn_amd kernels need ROCm's hipcc")
+    return found
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _compile(source: Path) -> Path:
+    obj = BUILD / (source.stem + ".o")
+    cmd = [hipcc(), *FLAGS, "-c", str(source), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {source.name}:\n{proc.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile all kernels and link the shared library; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = sources()
+    workers = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16) or 1
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(_compile, srcs))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

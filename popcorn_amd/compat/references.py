@@ -1,0 +1,64 @@
+"""Popcorn's registered PyTorch references for the four transformer-block ops.
+
+These are the op definitions of Popcorn: each is the `torch` implementation
+its dispatcher always holds, and what its harness evaluates on float64 clones
+for truth and at native dtype for the error budget. They are restated here in
+eager torch with the same sequence of tensor ops, because that sequence fixes
+the native-dtype rounding the budget measures:
+
+    rms_norm          kernels/rms_norm.py:16-30 (`rms`, `upcast`: kernels/_utils.py:6-16)
+    swiglu            kernels/swiglu.py:9-18
+    rotary_embedding  kernels/rotary_embedding.py:12-40
+    attn              kernels/attn.py:10-37
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+
+def upcast(t: Tensor) -> Tensor:
+    """The wider of t's dtype and fp32 (fp64 is kept)."""
+    return t.to(torch.promote_types(t.dtype, torch.float32))
+
+
+def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float = 1e-6) -> Tensor:
+    """Normalise in >= fp32, round to x's dtype, then scale (and shift) in that dtype."""
+    h = upcast(x)
+    inv_rms = torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)
+    y = (h * inv_rms).to(x.dtype) * weight
+    return y if bias is None else y + bias
+
+
+def swiglu(a: Tensor, b: Tensor) -> Tensor:
+    """silu(a) * b: two eager ops, so at 16-bit dtypes silu is rounded before the product."""
+    return F.silu(a) * b
+
+
+def rotary_embedding(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = False) -> Tensor:
+    """Rotate channel pairs in >= fp32 and round once; channels past 2*half pass through."""
+    half = cos.shape[-1]
+    c = upcast(cos.detach()).unsqueeze(1)  # [seq, 1, half], broadcast over batch and heads
+    s = upcast(sin.detach()).unsqueeze(1)
+    if interleaved:
+        u, v = upcast(x[..., 0 : 2 * half : 2]), upcast(x[..., 1 : 2 * half : 2])
+    else:
+        u, v = upcast(x[..., :half]), upcast(x[..., half : 2 * half])
+    first, second = u * c - v * s, u * s + v * c
+    if interleaved:
+        rotated = torch.stack((first, second), dim=-1).flatten(-2)
+    else:
+        rotated = torch.cat((first, second), dim=-1)
+    rotated = rotated.to(x.dtype)
+    if 2 * half == x.shape[-1]:
+        return rotated
+    return torch.cat((rotated, x[..., 2 * half :]), dim=-1)
+
+
+def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None) -> Tensor:
+    """torch SDPA on head-major views, grouped kv heads, returned in [batch, seq, heads, dim]."""
+    heads_first = [t.transpose(1, 2) for t in (q, k, v)]
+    out = F.scaled_dot_product_attention(*heads_first, scale=softmax_scale, is_causal=causal, enable_gqa=True)
+    return out.transpose(1, 2)

@@ -1,0 +1,183 @@
+// SwiGLU forward / backward: one HBM stream over n elements.
+//
+// Each thread moves UNROLL 16-byte vectors of every operand, all loads issued
+// before any arithmetic so a wave keeps 2*UNROLL (fwd) or 3*UNROLL (bwd)
+// 128-bit requests in flight. Data is touched once, so loads and stores are
+// non-temporal. A 1-block scalar launch finishes a ragged tail; unaligned
+// pointers take the scalar kernel for the whole range.
+#include "api.h"
+#include "common.h"
+
+namespace pk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+// sigmoid(a) in fp32 from the hardware exp2 and reciprocal (each ~1 ulp): the
+// stream is HBM-bound only while the per-element VALU work stays this short.
+__device__ __forceinline__ float sigmoid_f32(float a) { return __builtin_amdgcn_rcpf(1.0f + __expf(-a)); }
+
+// silu(a) = a * sigmoid(a), torch's a / (1 + exp(-a)) to within ~2 fp32 ulp.
+__device__ __forceinline__ float silu_f32(float a) { return a * sigmoid_f32(a); }
+
+// Forward element: torch eager rounds silu's result to T, then the product.
+template <typename T> __device__ __forceinline__ T fwd_elem(T a, T b) {
+  const float s = round_to<T>(silu_f32(to_f32(a)));
+  return from_f32<T>(s * to_f32(b));
+}
+
+template <typename T> __device__ __forceinline__ void bwd_elem(T g, T a, T b, T& da, T& db) {
+  const float af = to_f32(a), bf = to_f32(b), gf = to_f32(g);
+  const float s = sigmoid_f32(af);
+  da = from_f32<T>(gf * bf * s * (1.0f + af * (1.0f - s)));
+  db = from_f32<T>(gf * af * s);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const T* __restrict__ a, const T* __restrict__ b,
+                                                           T* __restrict__ y, int64_t nvec) {
+  constexpr int P = Vec<T>::N;
+  const int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+  Vec<T> va[kUnroll], vb[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      va[u] = ld16_stream(a + i * P);
+      vb[u] = ld16_stream(b + i * P);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      Vec<T> vy;
+#pragma unroll
+      for (int j = 0; j < P; ++j) vy.v[j] = fwd_elem(va[u].v[j], vb[u].v[j]);
+      st16_stream(y + i * P, vy);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(const T* __restrict__ a, const T* __restrict__ b,
+                                                              T* __restrict__ y, int64_t start, int64_t n) {
+  for (int64_t i = start + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    y[i] = fwd_elem(a[i], b[i]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(const T* __restrict__ g, const T* __restrict__ a,
+                                                           const T* __restrict__ b, T* __restrict__ da,
+                                                           T* __restrict__ db, int64_t nvec) {
+  constexpr int P = Vec<T>::N;
+  const int64_t base = (int64_t)blockIdx.x * (kThreads * kUnroll) + threadIdx.x;
+  Vec<T> vg[kUnroll], va[kUnroll], vb[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      vg[u] = ld16_stream(g + i * P);
+      va[u] = ld16_stream(a + i * P);
+      vb[u] = ld16_stream(b + i * P);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      Vec<T> vda, vdb;
+#pragma unroll
+      for (int j = 0; j < P; ++j) bwd_elem(vg[u].v[j], va[u].v[j], vb[u].v[j], vda.v[j], vdb.v[j]);
+      st16_stream(da + i * P, vda);
+      st16_stream(db + i * P, vdb);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(const T* __restrict__ g, const T* __restrict__ a,
+                                                              const T* __restrict__ b, T* __restrict__ da,
+                                                              T* __restrict__ db, int64_t start, int64_t n) {
+  for (int64_t i = start + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+    bwd_elem(g[i], a[i], b[i], da[i], db[i]);
+}
+
+int64_t blocks_for(int64_t work, int64_t per_block) { return (work + per_block - 1) / per_block; }
+
+template <typename T> int fwd(const void* a, const void* b, void* y, int64_t n, hipStream_t stream) {
+  constexpr int P = Vec<T>::N;
+  const T* ap = static_cast<const T*>(a);
+  const T* bp = static_cast<const T*>(b);
+  T* yp = static_cast<T*>(y);
+  const bool vec = aligned16(a) && aligned16(b) && aligned16(y);
+  const int64_t nvec = vec ? n / P : 0;
+  if (nvec > 0)
+    hipLaunchKernelGGL(swiglu_fwd_vec<T>, dim3(blocks_for(nvec, kThreads * kUnroll)), dim3(kThreads), 0, stream, ap,
+                       bp, yp, nvec);
+  const int64_t rest = n - nvec * P;
+  if (rest > 0) {
+    const int64_t grid = blocks_for(rest, kThreads) < 1024 ? blocks_for(rest, kThreads) : 1024;
+    hipLaunchKernelGGL(swiglu_fwd_scalar<T>, dim3(grid), dim3(kThreads), 0, stream, ap, bp, yp, nvec * P, n);
+  }
+  return launched("pk_swiglu_fwd");
+}
+
+template <typename T>
+int bwd(const void* g, const void* a, const void* b, void* da, void* db, int64_t n, hipStream_t stream) {
+  constexpr int P = Vec<T>::N;
+  const T* gp = static_cast<const T*>(g);
+  const T* ap = static_cast<const T*>(a);
+  const T* bp = static_cast<const T*>(b);
+  T* dap = static_cast<T*>(da);
+  T* dbp = static_cast<T*>(db);
+  const bool vec = aligned16(g) && aligned16(a) && aligned16(b) && aligned16(da) && aligned16(db);
+  const int64_t nvec = vec ? n / P : 0;
+  if (nvec > 0)
+    hipLaunchKernelGGL(swiglu_bwd_vec<T>, dim3(blocks_for(nvec, kThreads * kUnroll)), dim3(kThreads), 0, stream, gp,
+                       ap, bp, dap, dbp, nvec);
+  const int64_t rest = n - nvec * P;
+  if (rest > 0) {
+    const int64_t grid = blocks_for(rest, kThreads) < 1024 ? blocks_for(rest, kThreads) : 1024;
+    hipLaunchKernelGGL(swiglu_bwd_scalar<T>, dim3(grid), dim3(kThreads), 0, stream, gp, ap, bp, dap, dbp, nvec * P,
+                       n);
+  }
+  return launched("pk_swiglu_bwd");
+}
+
+}  // namespace
+}  // namespace pk
+
+extern "C" {
+
+int pk_swiglu_fwd(const void* a, const void* b, void* y, int64_t n, int dtype, void* stream) {
+  using namespace pk;
+  if (n < 0) return fail(PK_ERR_INVALID, "pk_swiglu_fwd: negative size %lld", (long long)n);
+  if (n == 0) return PK_OK;
+  if (!a || !b || !y) return fail(PK_ERR_INVALID, "pk_swiglu_fwd: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PK_F32: return fwd<float>(a, b, y, n, s);
+    case PK_BF16: return fwd<bf16>(a, b, y, n, s);
+    case PK_F16: return fwd<f16>(a, b, y, n, s);
+  }
+  return fail(PK_ERR_UNSUPPORTED, "pk_swiglu_fwd: dtype code %d", dtype);
+}
+
+int pk_swiglu_bwd(const void* dy, const void* a, const void* b, void* da, void* db, int64_t n, int dtype,
+                  void* stream) {
+  using namespace pk;
+  if (n < 0) return fail(PK_ERR_INVALID, "pk_swiglu_bwd: negative size %lld", (long long)n);
+  if (n == 0) return PK_OK;
+  if (!dy || !a || !b || !da || !db) return fail(PK_ERR_INVALID, "pk_swiglu_bwd: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PK_F32: return bwd<float>(dy, a, b, da, db, n, s);
+    case PK_BF16: return bwd<bf16>(dy, a, b, da, db, n, s);
+    case PK_F16: return bwd<f16>(dy, a, b, da, db, n, s);
+  }
+  return fail(PK_ERR_UNSUPPORTED, "pk_swiglu_bwd: dtype code %d", dtype);
+}
+
+}  // extern "C"

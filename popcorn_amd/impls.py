@@ -1,0 +1,318 @@
+"""MI355X implementations of Popcorn's transformer-block ops.
+
+Each public function has exactly the reference's signature, so Popcorn can
+register it as a bare `source=` (its leading parameters must equal the
+reference's names, core/dispatcher.py:184-201), and returns new tensors of the
+reference's output structure. Arithmetic happens in the HIP kernels of
+`libpopcorn_amd.so`, launched on torch's current stream; there is no
+host-side or torch fallback: an input the kernels do not cover raises.
+
+    rms_norm(x, weight, bias=None, eps=1e-6)        kernels/rms_norm.py:16-30
+    swiglu(a, b)                                    kernels/swiglu.py:9-18
+    rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
+    attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37 (forward only)
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from popcorn_amd import _lib
+
+__all__ = ["rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "rotary_embedding_"]
+
+
+def _require_cuda(*tensors: Tensor | None) -> torch.device:
+    devices = {t.device for t in tensors if t is not None}
+    if len(devices) != 1:
+        raise ValueError(f"popcorn_amd: tensors on several devices {sorted(map(str, devices))}")
+    device = devices.pop()
+    if device.type != "cuda":
+        raise ValueError(f"popcorn_amd: tensors must be on a HIP device, got {device}")
+    return device
+
+
+def _same_dtype(name: str, *tensors: Tensor | None) -> torch.dtype:
+    dtypes = {t.dtype for t in tensors if t is not None}
+    if len(dtypes) != 1:
+        raise TypeError(f"popcorn_amd.{name}: mixed dtypes {sorted(map(str, dtypes))}")
+    dtype = dtypes.pop()
+    _lib.dtype_code(dtype)
+    return dtype
+
+
+# --------------------------------------------------------------------------- rms_norm
+
+
+class _RMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, eps: float) -> Tensor:
+        device = _require_cuda(x, weight, bias)
+        dtype = _same_dtype("rms_norm", x, weight, bias)
+        cols = x.shape[-1]
+        if weight.shape != (cols,) or (bias is not None and bias.shape != (cols,)):
+            raise ValueError(f"popcorn_amd.rms_norm: weight/bias must be [{cols}]")
+        x2 = x.reshape(-1, cols).contiguous()
+        w = weight.contiguous()
+        b = bias.contiguous() if bias is not None else None
+        rows = x2.shape[0]
+        y = torch.empty_like(x2)
+        rstd = torch.empty(rows, dtype=torch.float32, device=device)
+        lib = _lib.load()
+        _lib.check(
+            lib.pk_rmsnorm_fwd(
+                x2.data_ptr(),
+                w.data_ptr(),
+                b.data_ptr() if b is not None else None,
+                y.data_ptr(),
+                rstd.data_ptr(),
+                rows,
+                cols,
+                float(eps),
+                _lib.dtype_code(dtype),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
+        ctx.save_for_backward(x2, w, rstd)
+        ctx.has_bias = b is not None
+        ctx.shape = x.shape
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy: Tensor):
+        x2, w, rstd = ctx.saved_tensors
+        rows, cols = x2.shape
+        dy2 = dy.reshape(rows, cols).to(x2.dtype).contiguous()
+        dx = torch.empty_like(x2)
+        dw = torch.empty_like(w)
+        db = torch.empty_like(w) if ctx.has_bias else None
+        if rows == 0:
+            dw.zero_()
+            if db is not None:
+                db.zero_()
+        else:
+            lib = _lib.load()
+            code = _lib.dtype_code(x2.dtype)
+            nbytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, code)
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+            _lib.check(
+                lib.pk_rmsnorm_bwd(
+                    x2.data_ptr(),
+                    w.data_ptr(),
+                    rstd.data_ptr(),
+                    dy2.data_ptr(),
+                    dx.data_ptr(),
+                    dw.data_ptr(),
+                    db.data_ptr() if db is not None else None,
+                    workspace.data_ptr(),
+                    nbytes,
+                    rows,
+                    cols,
+                    code,
+                    _lib.stream_handle(x2.device),
+                ),
+                lib,
+            )
+        return dx.view(ctx.shape), dw, db, None
+
+
+def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float = 1e-6) -> Tensor:
+    """y = round(round(x * rsqrt(mean(x^2) + eps)) * weight) [+ bias], fp32 statistics.
+
+    x [..., normalized_shape]; weight, bias [normalized_shape]; one dtype for all
+    (fp32, bf16 or fp16). Backward gives dx, dweight, dbias.
+    """
+    return _RMSNorm.apply(x, weight, bias, eps)
+
+
+# --------------------------------------------------------------------------- swiglu
+
+
+class _SwiGLU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a: Tensor, b: Tensor) -> Tensor:
+        device = _require_cuda(a, b)
+        dtype = _same_dtype("swiglu", a, b)
+        if a.shape != b.shape:
+            raise ValueError(f"popcorn_amd.swiglu: shapes differ {tuple(a.shape)} vs {tuple(b.shape)}")
+        a_c, b_c = a.contiguous(), b.contiguous()
+        y = torch.empty_like(a_c)
+        lib = _lib.load()
+        _lib.check(
+            lib.pk_swiglu_fwd(
+                a_c.data_ptr(), b_c.data_ptr(), y.data_ptr(), a_c.numel(), _lib.dtype_code(dtype),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
+        ctx.save_for_backward(a_c, b_c)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy: Tensor):
+        a_c, b_c = ctx.saved_tensors
+        g = dy.to(a_c.dtype).contiguous()
+        da, db = torch.empty_like(a_c), torch.empty_like(b_c)
+        lib = _lib.load()
+        _lib.check(
+            lib.pk_swiglu_bwd(
+                g.data_ptr(), a_c.data_ptr(), b_c.data_ptr(), da.data_ptr(), db.data_ptr(), a_c.numel(),
+                _lib.dtype_code(a_c.dtype), _lib.stream_handle(a_c.device),
+            ),
+            lib,
+        )
+        return da, db
+
+
+def swiglu(a: Tensor, b: Tensor) -> Tensor:
+    """y = silu(a) * b elementwise (a, b of one shape and dtype); differentiable."""
+    return _SwiGLU.apply(a, b)
+
+
+# --------------------------------------------------------------------------- rotary
+
+
+def _rotate(x: Tensor, cos: Tensor, sin: Tensor, out: Tensor, interleaved: bool, conjugate: bool) -> None:
+    device = _require_cuda(x, cos, sin, out)
+    if x.dim() != 4:
+        raise ValueError(f"popcorn_amd.rotary_embedding: x must be [batch, seq, heads, head_dim], got {tuple(x.shape)}")
+    batch, seq, heads, head_dim = x.shape
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[0] != seq:
+        raise ValueError(f"popcorn_amd.rotary_embedding: cos/sin must be [{seq}, half], got {tuple(cos.shape)}")
+    if cos.dtype != sin.dtype:
+        raise TypeError("popcorn_amd.rotary_embedding: cos and sin dtypes differ")
+    half = cos.shape[1]
+    if 2 * half > head_dim:
+        raise ValueError(f"popcorn_amd.rotary_embedding: half={half} > head_dim/2")
+    lib = _lib.load()
+    strides = (_lib._i64 * 6)(x.stride(0), x.stride(1), x.stride(2), out.stride(0), out.stride(1), out.stride(2))
+    _lib.check(
+        lib.pk_rotary(
+            x.data_ptr(),
+            cos.data_ptr(),
+            sin.data_ptr(),
+            out.data_ptr(),
+            strides,
+            batch,
+            seq,
+            heads,
+            head_dim,
+            half,
+            _lib.dtype_code(x.dtype),
+            _lib.dtype_code(cos.dtype),
+            int(interleaved),
+            int(conjugate),
+            _lib.stream_handle(device),
+        ),
+        lib,
+    )
+
+
+def _last_contiguous(t: Tensor) -> Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+class _Rotary(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool) -> Tensor:
+        xs = _last_contiguous(x)
+        cos_c, sin_c = cos.detach().contiguous(), sin.detach().contiguous()
+        y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        _rotate(xs, cos_c, sin_c, y, interleaved, conjugate=False)
+        ctx.save_for_backward(cos_c, sin_c)
+        ctx.interleaved = interleaved
+        return y
+
+    @staticmethod
+    def backward(ctx, dy: Tensor):
+        cos_c, sin_c = ctx.saved_tensors
+        g = _last_contiguous(dy)
+        dx = torch.empty(dy.shape, dtype=dy.dtype, device=dy.device)
+        _rotate(g, cos_c, sin_c, dx, ctx.interleaved, conjugate=True)
+        return dx, None, None, None
+
+
+def rotary_embedding(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = False) -> Tensor:
+    """Rotate x [batch, seq, heads, head_dim] by cos/sin [seq, half] (fp32 math, one rounding).
+
+    NeoX halves by default, GPT-J pairs with interleaved=True; channels past
+    2*half are passed through. Returns a new tensor; cos and sin get no gradient.
+    """
+    return _Rotary.apply(x, cos, sin, interleaved)
+
+
+def rotary_embedding_(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = False) -> Tensor:
+    """In-place variant of `rotary_embedding` (no autograd): x is overwritten and returned."""
+    if torch.is_grad_enabled() and x.requires_grad:
+        raise RuntimeError("popcorn_amd.rotary_embedding_: in-place rotation of a tensor that requires grad")
+    if x.stride(-1) != 1:
+        raise ValueError("popcorn_amd.rotary_embedding_: last dimension must be contiguous")
+    _rotate(x, cos.contiguous(), sin.contiguous(), x, interleaved, conjugate=False)
+    return x
+
+
+# --------------------------------------------------------------------------- attention
+
+
+def attn_with_lse(
+    q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None
+) -> tuple[Tensor, Tensor]:
+    """Forward attention returning (o [batch, seq, q_heads, head_dim], lse [batch, q_heads, seq] fp32)."""
+    return _attention(q, k, v, causal, softmax_scale, want_lse=True)
+
+
+def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None) -> Tensor:
+    """softmax(q k^T * scale + causal mask) v with grouped kv heads; forward only.
+
+    q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim];
+    bf16 or fp16; head_dim 64 or 128; scale defaults to head_dim ** -0.5.
+    """
+    return _attention(q, k, v, causal, softmax_scale, want_lse=False)[0]
+
+
+def _attention(q, k, v, causal, softmax_scale, want_lse):
+    device = _require_cuda(q, k, v)
+    dtype = _same_dtype("attn", q, k, v)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise RuntimeError("popcorn_amd.attn is forward-only; call it under torch.no_grad() or on detached inputs")
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise ValueError("popcorn_amd.attn: q [b, s, hq, d] and k, v [b, s, hkv, d] expected")
+    batch, seq, q_heads, head_dim = q.shape
+    if k.shape[0] != batch or k.shape[1] != seq or k.shape[3] != head_dim:
+        raise ValueError(f"popcorn_amd.attn: k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    kv_heads = k.shape[2]
+    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+    q_, k_, v_ = (_aligned_rows(t) for t in (q, k, v))
+    o = torch.empty((batch, seq, q_heads, head_dim), dtype=dtype, device=device)
+    lse = torch.empty((batch, q_heads, seq), dtype=torch.float32, device=device) if want_lse else None
+    lib = _lib.load()
+    strides = (_lib._i64 * 12)(*(s for t in (q_, k_, v_, o) for s in t.stride()[:3]))
+    _lib.check(
+        lib.pk_attn_fwd(
+            q_.data_ptr(),
+            k_.data_ptr(),
+            v_.data_ptr(),
+            o.data_ptr(),
+            lse.data_ptr() if lse is not None else None,
+            strides,
+            batch,
+            seq,
+            q_heads,
+            kv_heads,
+            head_dim,
+            scale,
+            int(bool(causal)),
+            _lib.dtype_code(dtype),
+            _lib.stream_handle(device),
+        ),
+        lib,
+    )
+    return o, lse
+
+
+def _aligned_rows(t: Tensor) -> Tensor:
+    """A view the kernel can read with 16-byte loads, copying only when it must."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 and s >= 0 for s in t.stride()[:3])
+    return t if ok else t.contiguous()
