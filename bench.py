@@ -1,0 +1,408 @@
+"""Benchmark of the MI355X transformer-block kernels on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-others]
+
+A step is one pass of a workload's drop-in call (the `popcorn_amd.impls`
+function Popcorn dispatches to) over one batch of synthetic input already
+resident in HBM. The default workload is BASELINE config 2 (SwiGLU forward,
+bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, or `copy`, a
+plain device copy of known size used to calibrate HBM byte counters.
+
+Rank 0 prints ONE JSON line. `value` is the workload's achieved algorithmic
+throughput (TB/s of HBM bytes for c1-c4, TFLOP/s for c5). `roofline` is the
+dominant kernel's figure, timed with HIP events on the stream it is launched
+on (torch's current stream). `cpu_baseline` times Popcorn's PyTorch reference
+(the `torch` implementation its dispatcher always holds, restated in
+popcorn_amd.compat.references) on the host's cores over a bounded row sample
+of the same workload. `others` holds the remaining configs' kernel figures.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from dataclasses import dataclass, field
+from typing import Callable
+
+import torch
+
+HBM_PEAK_TBS = 8.0  # MI355X HBM3E, TB/s
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "achieved HBM TB/s (norm/rope/swiglu) + attn-fwd bf16 TFLOP/s, % of peak"
+FLUSH_BYTES = 512 << 20  # inputs of a workload are rotated until they exceed the 256 MB MALL twice over
+
+# HBM bytes per launch of each dominant kernel, from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE runs scaled by the same counters' reading for a plain device
+# copy (profiles/hbm_traffic.md). None until measured for that kernel.
+MEASURED_TRAFFIC: dict[str, int | None] = {}
+
+
+@dataclass
+class Workload:
+    name: str
+    description: str
+    dtype: str
+    unit: str  # "TB/s" or "TFLOP/s"
+    work: float  # algorithmic bytes (TB/s units) or FLOPs per step
+    step: Callable[[int], None]  # step(i): one pass of the drop-in call on input copy i
+    kernel: str  # dominant kernel's name (as rocprofv3 reports it, prefix)
+    kernel_work: float  # algorithmic bytes / FLOPs of one launch of that kernel
+    launch: Callable[[int], None]  # one launch of the dominant kernel alone on input copy i
+    config: dict = field(default_factory=dict)
+    cpu: Callable[[], tuple[float, str]] | None = None  # -> (throughput in unit, sample description)
+
+
+def _copies(nbytes: int) -> int:
+    """Input copies to rotate so one sweep over them does not fit in the MALL."""
+    return max(1, math.ceil(FLUSH_BYTES / max(nbytes, 1)))
+
+
+def _randn(shape, dtype, gen, dev):
+    return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).to(dtype)
+
+
+def make_workload(name: str, dev: torch.device) -> Workload:
+    from popcorn_amd import _lib, impls
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    lib = _lib.load()
+    stream = lambda: _lib.stream_handle(dev)  # noqa: E731
+
+    if name == "c1":
+        rows, cols = 4096, 4096
+        nbytes = rows * cols * 4 * 2 + cols * 4
+        n = _copies(nbytes)
+        xs = [_randn((rows, cols), torch.float32, gen, dev) for _ in range(n)]
+        w = 1 + 0.1 * _randn((cols,), torch.float32, gen, dev)
+        y = torch.empty_like(xs[0])
+
+        def step(i):
+            impls.rms_norm(xs[i % n], w, None, 1e-6)
+
+        def launch(i):
+            _lib.check(lib.pk_rmsnorm_fwd(xs[i % n].data_ptr(), w.data_ptr(), None, y.data_ptr(), None, rows, cols,
+                                          1e-6, _lib.F32, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            xc = torch.randn(rows, cols)
+            wc = 1 + 0.1 * torch.randn(cols)
+            t, reps = _time_cpu(lambda: R.rms_norm(xc, wc, None, 1e-6))
+            return nbytes / t / 1e12, f"full C1 x [{rows}, {cols}] fp32, median of {reps} reps"
+
+        return Workload("c1", "RMSNorm forward fp32 x [4096, 4096]", "f32", "TB/s", nbytes, step,
+                        "rmsnorm_fwd_vec", nbytes, launch,
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "fp32"}, cpu)
+
+    if name == "c2":
+        rows, cols = 16384, 14336
+        numel = rows * cols
+        nbytes = 3 * numel * 2
+        a = _randn((rows, cols), torch.bfloat16, gen, dev)
+        b = _randn((rows, cols), torch.bfloat16, gen, dev)
+        y = torch.empty_like(a)
+
+        def step(i):
+            impls.swiglu(a, b)
+
+        def launch(i):
+            _lib.check(lib.pk_swiglu_fwd(a.data_ptr(), b.data_ptr(), y.data_ptr(), numel, _lib.BF16, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            sample_rows = 1024
+            ac = torch.randn(sample_rows, cols).bfloat16()
+            bc = torch.randn(sample_rows, cols).bfloat16()
+            t, reps = _time_cpu(lambda: R.swiglu(ac, bc))
+            return 3 * sample_rows * cols * 2 / t / 1e12, f"{sample_rows} of {rows} rows x {cols} bf16, median of {reps} reps"
+
+        return Workload("c2", "SwiGLU forward bf16 a, b [16384, 14336]", "bf16", "TB/s", nbytes, step,
+                        "swiglu_fwd_vec", nbytes, launch, {"rows": rows, "cols": cols, "dtype": "bf16"}, cpu)
+
+    if name == "c3":
+        B, S, HQ, HKV, D, half = 8, 4096, 32, 8, 128, 64
+        q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
+        k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        pos = torch.arange(S, dtype=torch.float64)[:, None]
+        inv_freq = 500000.0 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+        ang = pos * inv_freq[None, :]
+        cos, sin = ang.cos().float().to(dev), ang.sin().float().to(dev)
+        qb, kb = q.numel() * 2, k.numel() * 2
+        table = 2 * S * half * 4
+        nbytes = 2 * qb + 2 * kb + 2 * table
+        yq, yk = torch.empty_like(q), torch.empty_like(k)
+
+        def step(i):
+            impls.rotary_embedding(q, cos, sin)
+            impls.rotary_embedding(k, cos, sin)
+
+        def rot(x, y):
+            strides = (_lib._i64 * 6)(x.stride(0), x.stride(1), x.stride(2), y.stride(0), y.stride(1), y.stride(2))
+            _lib.check(lib.pk_rotary(x.data_ptr(), cos.data_ptr(), sin.data_ptr(), y.data_ptr(), strides, B, S,
+                                     x.shape[2], D, half, _lib.BF16, _lib.F32, 0, 0, stream()))
+
+        def launch(i):
+            rot(q, yq)
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            sb = 1
+            qc = torch.randn(sb, S, HQ, D).bfloat16()
+            kc = torch.randn(sb, S, HKV, D).bfloat16()
+            cc, sc = cos.cpu(), sin.cpu()
+            t, reps = _time_cpu(lambda: (R.rotary_embedding(qc, cc, sc), R.rotary_embedding(kc, cc, sc)))
+            work = 2 * (qc.numel() + kc.numel()) * 2 + 2 * table
+            return work / t / 1e12, f"batch 1 of {B} (q and k calls), median of {reps} reps"
+
+        return Workload("c3", "Rotary NeoX bf16 q [8,4096,32,128] + k [8,4096,8,128], fp32 cos/sin [4096,64]",
+                        "bf16", "TB/s", nbytes, step, "rotary_kernel", 2 * qb + table, launch,
+                        {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "theta": 500000.0,
+                         "dtype": "bf16", "tables": "fp32"}, cpu)
+
+    if name == "c4":
+        rows, cols = 65536, 8192
+        x = _randn((rows, cols), torch.bfloat16, gen, dev)
+        w = (1 + 0.1 * _randn((cols,), torch.float32, gen, dev)).bfloat16()
+        dy = _randn((rows, cols), torch.bfloat16, gen, dev)
+        elems = rows * cols
+        fwd_bytes = 2 * elems * 2 + cols * 2
+        bwd_bytes = 3 * elems * 2 + cols * 2 + cols * 4
+        xg = x.detach().requires_grad_()
+        wg = w.detach().requires_grad_()
+        y = torch.empty_like(x)
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(w)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        _lib.check(lib.pk_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), rstd.data_ptr(), rows, cols,
+                                      1e-6, _lib.BF16, stream()))
+        ws_bytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, _lib.BF16)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+        def step(i):
+            yy = impls.rms_norm(xg, wg, None, 1e-6)
+            torch.autograd.grad(yy, (xg, wg), dy)
+
+        def launch(i):
+            _lib.check(lib.pk_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(), dx.data_ptr(),
+                                          dw.data_ptr(), None, ws.data_ptr(), ws_bytes, rows, cols, _lib.BF16,
+                                          stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            sample = 2048
+            xc = torch.randn(sample, cols).bfloat16().requires_grad_()
+            wc = (1 + 0.1 * torch.randn(cols)).bfloat16().requires_grad_()
+            gc = torch.randn(sample, cols).bfloat16()
+
+            def one():
+                yc = R.rms_norm(xc, wc, None, 1e-6)
+                torch.autograd.grad(yc, (xc, wc), gc)
+
+            t, reps = _time_cpu(one)
+            work = 5 * sample * cols * 2 + 2 * cols * 2 + cols * 4
+            return work / t / 1e12, f"{sample} of {rows} rows x {cols} bf16, fwd+bwd, median of {reps} reps"
+
+        return Workload("c4", "RMSNorm fwd+bwd bf16 x, dy [65536, 8192]", "bf16", "TB/s", fwd_bytes + bwd_bytes,
+                        step, "rmsnorm_bwd_vec", bwd_bytes, launch,
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu)
+
+    if name == "c5":
+        B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
+        q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
+        k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        flops = 4.0 * B * HQ * D * S * S / 2
+        o = torch.empty_like(q)
+        lse = torch.empty((B, HQ, S), dtype=torch.float32, device=dev)
+        strides = (_lib._i64 * 12)(*(s for t in (q, k, v, o) for s in t.stride()[:3]))
+
+        def step(i):
+            with torch.no_grad():
+                impls.attn_with_lse(q, k, v, True)
+
+        def launch(i):
+            _lib.check(lib.pk_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            s_cpu = 2048
+            qc = torch.randn(1, s_cpu, HQ, D).bfloat16()
+            kc = torch.randn(1, s_cpu, HKV, D).bfloat16()
+            vc = torch.randn(1, s_cpu, HKV, D).bfloat16()
+            t, reps = _time_cpu(lambda: R.attn(qc, kc, vc, True), min_reps=2)
+            work = 4.0 * HQ * D * s_cpu * s_cpu / 2
+            return work / t / 1e12, f"B=1, S={s_cpu} (of B=4, S=8192), causal, median of {reps} reps"
+
+        return Workload("c5", "Causal GQA attention fwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16", "TFLOP/s",
+                        flops, step, "attn_fwd_kernel", flops, launch,
+                        {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
+                         "dtype": "bf16"}, cpu)
+
+    if name == "copy":
+        numel = 256 << 20  # 512 MiB of bf16 each way
+        src = torch.empty(numel, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        nbytes = 2 * numel * 2
+
+        def step(i):
+            dst.copy_(src)
+
+        return Workload("copy", "plain device copy, 512 MiB -> 512 MiB", "bf16", "TB/s", nbytes, step, "copy",
+                        nbytes, step, {"bytes_each_way": numel * 2})
+
+    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, copy)")
+
+
+def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 20) -> tuple[float, int]:
+    """Median wall time of fn on the CPU after one warmup, over reps filling about budget_s."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    reps = int(min(max_reps, max(min_reps, budget_s / max(first, 1e-6))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], reps
+
+
+def _time_gpu(fn: Callable[[int], None], steps: int, warmup: int) -> tuple[float, list[float]]:
+    """Total ms for `steps` back-to-back calls and each call's ms, from HIP events on torch's current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record()
+        fn(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    each = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return starts[0].elapsed_time(ends[-1]), each
+
+
+def _rate(work: float, ms: float, unit: str) -> float:
+    return work / (ms * 1e-3) / 1e12
+
+
+def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
+    _, each = _time_gpu(wl.launch, steps, warmup)
+    avg = sum(each) / len(each)
+    achieved = _rate(wl.kernel_work, avg, wl.unit)
+    hbm = wl.unit == "TB/s"
+    peak = HBM_PEAK_TBS if hbm else BF16_PEAK_TFLOPS
+    return {
+        "kernel": wl.kernel,
+        "bound": "hbm" if hbm else "mfma",
+        "achieved": round(achieved * (1000 if hbm else 1), 2),
+        "peak": peak * (1000 if hbm else 1),
+        "unit": "GB/s" if hbm else "TFLOP/s",
+        "frac": round(achieved / peak, 4),
+        "avg_launch_us": round(avg * 1e3, 2),
+        "work_per_launch": wl.kernel_work,
+        "traffic": MEASURED_TRAFFIC.get(wl.kernel),
+    }
+
+
+def _cpu_baseline(wl: Workload) -> dict | None:
+    if wl.cpu is None:
+        return None
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    threads = max(1, min(affinity, 16))
+    torch.set_num_threads(threads)
+    value, sample = wl.cpu()
+    return {"value": round(value, 6), "unit": wl.unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"popcorn reference (torch, CPU): {sample}; host os.cpu_count()={os.cpu_count()}"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
+    ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; every config's kernels run on a single MI355X "
+              "(multi-GPU sharding is described, not run). Use --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    print(f"bench: workload {args.workload}, {args.warmup} warmup + {args.steps} steps", file=sys.stderr, flush=True)
+    wl = make_workload(args.workload, dev)
+    torch.cuda.synchronize()
+    total_ms, _ = _time_gpu(wl.step, args.steps, args.warmup)
+    ms_per_step = total_ms / args.steps
+    value = _rate(wl.work, ms_per_step, wl.unit)
+    print(f"bench: {wl.name} {ms_per_step:.4f} ms/step, {value:.3f} {wl.unit}", file=sys.stderr, flush=True)
+    roof = _roofline(wl, args.steps, args.warmup)
+    print(f"bench: {wl.kernel} {roof['avg_launch_us']} us/launch, frac {roof['frac']}", file=sys.stderr, flush=True)
+
+    others = {}
+    if not args.no_others and wl.name != "copy":
+        for name in ("c1", "c2", "c3", "c4", "c5"):
+            if name == wl.name:
+                continue
+            del wl
+            torch.cuda.empty_cache()
+            wl_o = make_workload(name, dev)
+            tot, _ = _time_gpu(wl_o.step, max(5, args.steps // 2), 2)
+            per = tot / max(5, args.steps // 2)
+            r = _roofline(wl_o, max(5, args.steps // 2), 2)
+            others[name] = {"workload": wl_o.description, "ms_per_step": round(per, 4),
+                            "value": round(_rate(wl_o.work, per, wl_o.unit), 4), "unit": wl_o.unit,
+                            "roofline": r}
+            print(f"bench: {name} {per:.4f} ms/step; {r['kernel']} frac {r['frac']}", file=sys.stderr, flush=True)
+            wl = wl_o
+        del wl
+        torch.cuda.empty_cache()
+        wl = make_workload(args.workload, dev)
+
+    cpu = None if args.no_cpu else _cpu_baseline(wl)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": wl.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.dtype,
+        "data": "synthetic N(0,1) inputs, seeded device generator, resident in HBM",
+        "config": {"workload": wl.description, **wl.config},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "others": others,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,308 @@
+"""Pins the float64 CPU oracle (oracle/reference.py) against facts it does not restate.
+
+Each oracle function is checked against at least one independent route to the
+same numbers (a library routine, a different formulation, finite differences
+or a closed-form special case), chosen so that a plausible slip in the oracle
+-- a dropped eps, a transposed operand, a sign error, a wrong GQA head map, an
+off-by-one in the causal mask -- fails at least one test. The last test plants
+such slips in copies of the oracle and shows the checks catch them.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import scipy.special
+import torch
+import torch.nn.functional as F
+
+from oracle import reference as O
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# --------------------------------------------------------------------------- rms_norm
+
+
+def test_rms_norm_matches_torch_functional():
+    r = rng(1)
+    x = r.standard_normal((5, 3, 48))
+    w = 1 + 0.1 * r.standard_normal(48)
+    for eps in (1e-6, 1e-5, 0.3):
+        want = F.rms_norm(torch.from_numpy(x), (48,), torch.from_numpy(w), eps=eps).numpy()
+        np.testing.assert_allclose(O.rms_norm(x, w, None, eps), want, rtol=1e-13, atol=1e-13)
+
+
+def test_rms_norm_bias_is_added_after_scaling():
+    r = rng(2)
+    x, w, b = r.standard_normal((4, 16)), r.standard_normal(16), r.standard_normal(16)
+    np.testing.assert_allclose(O.rms_norm(x, w, b) - O.rms_norm(x, w), np.broadcast_to(b, x.shape), atol=1e-14)
+
+
+def test_rms_norm_output_rms_closed_form():
+    """With w = 1: rms(y) = sqrt(ms / (ms + eps)) where ms = mean(x^2)."""
+    r = rng(3)
+    x = r.standard_normal((7, 33)) * np.arange(1, 8)[:, None]
+    eps = 0.05
+    y = O.rms_norm(x, np.ones(33), None, eps)
+    ms = np.mean(x * x, axis=-1)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), np.sqrt(ms / (ms + eps)), rtol=1e-13)
+
+
+def test_rms_norm_scale_invariance_and_zero_row():
+    r = rng(4)
+    x, w = r.standard_normal((3, 64)), r.standard_normal(64)
+    np.testing.assert_allclose(O.rms_norm(7.5 * x, w, None, 0.0), O.rms_norm(x, w, None, 0.0), rtol=1e-12)
+    z = O.rms_norm(np.zeros((2, 64)), w, None, 1e-6)
+    assert np.all(z == 0)
+
+
+def _finite_diff(f, x, h=1e-6):
+    g = np.zeros_like(x)
+    flat, gf = x.reshape(-1), g.reshape(-1)
+    for i in range(flat.size):
+        old = flat[i]
+        flat[i] = old + h
+        up = f()
+        flat[i] = old - h
+        down = f()
+        flat[i] = old
+        gf[i] = (up - down) / (2 * h)
+    return g
+
+
+def test_rms_norm_bwd_finite_differences():
+    r = rng(5)
+    x, w, b = r.standard_normal((3, 8)), 1 + 0.2 * r.standard_normal(8), r.standard_normal(8)
+    dy = r.standard_normal((3, 8))
+    eps = 1e-2
+    loss = lambda: float(np.sum(O.rms_norm(x, w, b, eps) * dy))  # noqa: E731
+    dx, dw, db = O.rms_norm_bwd(x, w, dy, eps)
+    np.testing.assert_allclose(dx, _finite_diff(loss, x), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(dw, _finite_diff(loss, w), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(db, _finite_diff(loss, b), rtol=1e-6, atol=1e-8)
+
+
+def test_rms_norm_bwd_matches_torch_autograd():
+    r = rng(6)
+    x, w, dy = r.standard_normal((2, 5, 32)), r.standard_normal(32), r.standard_normal((2, 5, 32))
+    xt, wt = torch.from_numpy(x).requires_grad_(), torch.from_numpy(w).requires_grad_()
+    y = F.rms_norm(xt, (32,), wt, eps=1e-6)
+    gx, gw = torch.autograd.grad(y, (xt, wt), torch.from_numpy(dy))
+    dx, dw, _ = O.rms_norm_bwd(x, w, dy, 1e-6)
+    np.testing.assert_allclose(dx, gx.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(dw, gw.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_rms_norm_bwd_orthogonal_to_x():
+    """With w = 1 and eps = 0, y is invariant to scaling x, so <dx, x> = 0 per row."""
+    r = rng(7)
+    x, dy = r.standard_normal((4, 40)), r.standard_normal((4, 40))
+    dx, _, _ = O.rms_norm_bwd(x, np.ones(40), dy, 0.0)
+    np.testing.assert_allclose(np.sum(dx * x, axis=-1), 0.0, atol=1e-12)
+
+
+# --------------------------------------------------------------------------- swiglu
+
+
+def test_swiglu_matches_expit():
+    a = np.linspace(-80, 80, 2001)
+    b = rng(8).standard_normal(a.shape)
+    np.testing.assert_allclose(O.swiglu(a, b), a * scipy.special.expit(a) * b, rtol=1e-14, atol=1e-300)
+
+
+def test_swiglu_special_values():
+    b = np.ones(4)
+    y = O.swiglu(np.array([0.0, 50.0, -50.0, 1.0]), b)
+    assert y[0] == 0.0
+    assert abs(y[1] - 50.0) < 1e-15 * 50
+    assert abs(y[2]) < 1e-19
+    assert abs(y[3] - 1.0 / (1.0 + np.exp(-1.0))) < 1e-15
+
+
+def test_swiglu_bwd_finite_differences_and_autograd():
+    r = rng(9)
+    a, b, g = r.standard_normal((3, 7)) * 3, r.standard_normal((3, 7)), r.standard_normal((3, 7))
+    loss = lambda: float(np.sum(O.swiglu(a, b) * g))  # noqa: E731
+    da, db = O.swiglu_bwd(g, a, b)
+    np.testing.assert_allclose(da, _finite_diff(loss, a), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(db, _finite_diff(loss, b), rtol=1e-6, atol=1e-8)
+    at, bt = torch.from_numpy(a).requires_grad_(), torch.from_numpy(b).requires_grad_()
+    gat, gbt = torch.autograd.grad(F.silu(at) * bt, (at, bt), torch.from_numpy(g))
+    np.testing.assert_allclose(da, gat.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(db, gbt.numpy(), rtol=1e-12, atol=1e-14)
+
+
+# --------------------------------------------------------------------------- rotary
+
+
+def _tables(seq, half, theta=10000.0):
+    pos = np.arange(seq)[:, None]
+    ang = pos * theta ** (-np.arange(half) / half)
+    return np.cos(ang), np.sin(ang)
+
+
+def test_rotary_neox_is_complex_multiplication():
+    r = rng(10)
+    x = r.standard_normal((2, 6, 3, 16))
+    c, s = r.standard_normal((6, 8)), r.standard_normal((6, 8))
+    z = (x[..., :8] + 1j * x[..., 8:]) * (c + 1j * s)[None, :, None, :]
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    np.testing.assert_allclose(O.rotary_embedding(x, c, s), want, rtol=1e-13, atol=1e-13)
+
+
+def test_rotary_interleaved_is_complex_multiplication_of_pairs():
+    r = rng(11)
+    x = r.standard_normal((1, 5, 2, 12))
+    c, s = r.standard_normal((5, 6)), r.standard_normal((5, 6))
+    z = (x[..., 0::2] + 1j * x[..., 1::2]) * (c + 1j * s)[None, :, None, :]
+    want = np.stack([z.real, z.imag], axis=-1).reshape(x.shape)
+    np.testing.assert_allclose(O.rotary_embedding(x, c, s, interleaved=True), want, rtol=1e-13, atol=1e-13)
+
+
+def test_rotary_identity_tables_and_partial_passthrough():
+    r = rng(12)
+    x = r.standard_normal((2, 4, 3, 20))
+    c, s = np.ones((4, 6)), np.zeros((4, 6))
+    np.testing.assert_array_equal(O.rotary_embedding(x, c, s), x)
+    c2, s2 = _tables(4, 6)
+    y = O.rotary_embedding(x, c2, s2)
+    np.testing.assert_array_equal(y[..., 12:], x[..., 12:])
+    assert not np.allclose(y[..., :12], x[..., :12])
+
+
+def test_rotary_unit_tables_preserve_pair_norms_and_conjugate_inverts():
+    r = rng(13)
+    x = r.standard_normal((2, 9, 4, 32))
+    c, s = _tables(9, 16, 500000.0)
+    for il in (False, True):
+        y = O.rotary_embedding(x, c, s, il)
+        if il:
+            nx, ny = x[..., 0::2] ** 2 + x[..., 1::2] ** 2, y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+        else:
+            nx, ny = x[..., :16] ** 2 + x[..., 16:] ** 2, y[..., :16] ** 2 + y[..., 16:] ** 2
+        np.testing.assert_allclose(ny, nx, rtol=1e-12)
+        np.testing.assert_allclose(O.rotary_embedding_bwd(y, c, s, il), x, rtol=1e-12, atol=1e-12)
+
+
+def test_rotary_bwd_is_transpose_by_finite_differences():
+    r = rng(14)
+    x = r.standard_normal((1, 3, 2, 8))
+    c, s, g = r.standard_normal((3, 4)), r.standard_normal((3, 4)), r.standard_normal((1, 3, 2, 8))
+    for il in (False, True):
+        loss = lambda: float(np.sum(O.rotary_embedding(x, c, s, il) * g))  # noqa: E731
+        np.testing.assert_allclose(O.rotary_embedding_bwd(g, c, s, il), _finite_diff(loss, x), rtol=1e-6, atol=1e-8)
+
+
+# --------------------------------------------------------------------------- attention
+
+
+def _sdpa64(q, k, v, causal, scale):
+    """float64 torch SDPA on [B, H, S, D] with kv heads repeated per group."""
+    group = q.shape[2] // k.shape[2]
+    qt = torch.from_numpy(q).transpose(1, 2)
+    kt = torch.from_numpy(k).repeat_interleave(group, dim=2).transpose(1, 2)
+    vt = torch.from_numpy(v).repeat_interleave(group, dim=2).transpose(1, 2)
+    return F.scaled_dot_product_attention(qt, kt, vt, is_causal=causal, scale=scale).transpose(1, 2).numpy()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [None, 0.25])
+def test_attention_matches_float64_sdpa(causal, scale):
+    r = rng(15)
+    q, k, v = r.standard_normal((2, 11, 6, 8)), r.standard_normal((2, 11, 2, 8)), r.standard_normal((2, 11, 2, 8))
+    o, lse = O.attention(q, k, v, causal, scale)
+    np.testing.assert_allclose(o, _sdpa64(q, k, v, causal, scale), rtol=1e-12, atol=1e-12)
+    # lse against scipy's logsumexp of explicitly masked scores
+    sc = 8**-0.5 if scale is None else scale
+    for b, h in [(0, 0), (1, 5)]:
+        s = q[b, :, h] @ k[b, :, h // 3].T * sc
+        if causal:
+            s = np.where(np.triu(np.ones((11, 11), bool), 1), -np.inf, s)
+        np.testing.assert_allclose(lse[b, h], scipy.special.logsumexp(s, axis=-1), rtol=1e-13)
+
+
+def test_attention_rows_agree_with_full():
+    r = rng(16)
+    q, k, v = r.standard_normal((1, 13, 4, 8)), r.standard_normal((1, 13, 1, 8)), r.standard_normal((1, 13, 1, 8))
+    o, lse = O.attention(q, k, v, True)
+    rows = np.array([0, 5, 12])
+    oo, ll = O.attention_rows(q[0, :, 3], k[0, :, 0], v[0, :, 0], rows, True)
+    np.testing.assert_allclose(oo, o[0, rows, 3], rtol=1e-13)
+    np.testing.assert_allclose(ll, lse[0, 3, rows], rtol=1e-13)
+
+
+def test_attention_special_cases():
+    r = rng(17)
+    s, d = 9, 4
+    v = r.standard_normal((1, s, 1, d))
+    k = r.standard_normal((1, s, 1, d))
+    o, lse = O.attention(np.zeros((1, s, 2, d)), k, v, True)
+    prefix = np.cumsum(v[0, :, 0], axis=0) / np.arange(1, s + 1)[:, None]
+    np.testing.assert_allclose(o[0, :, 1], prefix, rtol=1e-13)
+    np.testing.assert_allclose(lse[0, 0], np.log(np.arange(1, s + 1)), rtol=1e-13)
+    # the first query sees only key 0 under the causal mask
+    q = r.standard_normal((1, s, 2, d))
+    o, _ = O.attention(q, k, v, True)
+    np.testing.assert_allclose(o[0, 0, 0], v[0, 0, 0], rtol=1e-13)
+    # a single position: o = v
+    o1, l1 = O.attention(q[:, :1], k[:, :1], v[:, :1], False)
+    np.testing.assert_allclose(o1[0, 0, 1], v[0, 0, 0], rtol=1e-13)
+
+
+def test_attention_gqa_head_map():
+    """q head h reads kv head h // group, not h % kv_heads."""
+    r = rng(18)
+    q = r.standard_normal((1, 5, 4, 8))
+    k, v = r.standard_normal((1, 5, 2, 8)), r.standard_normal((1, 5, 2, 8))
+    o, _ = O.attention(q, k, v, False)
+    o1, _ = O.attention(q[:, :, 1:2], k[:, :, 0:1], v[:, :, 0:1], False)
+    np.testing.assert_allclose(o[:, :, 1:2], o1, rtol=1e-13)
+
+
+# --------------------------------------------------------------------------- planted mistakes
+
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    """Copies of the oracle with a typical slip each fail one of the checks above."""
+    r = rng(19)
+    x, w = r.standard_normal((3, 16)), 1 + 0.1 * r.standard_normal(16)
+
+    # rms_norm without eps
+    bad = lambda x, w, b=None, eps=1e-6: x / np.sqrt(np.mean(x * x, -1, keepdims=True)) * w  # noqa: E731
+    want = F.rms_norm(torch.from_numpy(x), (16,), torch.from_numpy(w), eps=0.3).numpy()
+    assert not np.allclose(bad(x, w, None, 0.3), want, rtol=1e-6)
+
+    # rotary with the sign of sin flipped
+    xr = r.standard_normal((1, 3, 2, 8))
+    c, s = r.standard_normal((3, 4)), r.standard_normal((3, 4))
+    flipped = O.rotary_embedding(xr, c, -s)
+    z = (xr[..., :4] + 1j * xr[..., 4:]) * (c + 1j * s)[None, :, None, :]
+    assert not np.allclose(flipped, np.concatenate([z.real, z.imag], -1))
+
+    # attention with kv head h % kv_heads instead of h // group
+    q = r.standard_normal((1, 5, 4, 8))
+    k, v = r.standard_normal((1, 5, 2, 8)), r.standard_normal((1, 5, 2, 8))
+    k_mod = k[:, :, [0, 1, 0, 1]]
+    v_mod = v[:, :, [0, 1, 0, 1]]
+    o_bad, _ = O.attention(q, k_mod, v_mod, False)
+    assert not np.allclose(o_bad, _sdpa64(q, k, v, False, None))
+
+    # causal mask shifted by one (diagonal excluded)
+    o_good, _ = O.attention(q, k, v, True)
+    qt = torch.from_numpy(q).transpose(1, 2)
+    kt = torch.from_numpy(k).repeat_interleave(2, 2).transpose(1, 2)
+    vt = torch.from_numpy(v).repeat_interleave(2, 2).transpose(1, 2)
+    strict = torch.ones(5, 5, dtype=torch.bool).tril(-1)
+    strict[0, 0] = True  # keep row 0 defined
+    o_shift = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=strict).transpose(1, 2).numpy()
+    assert not np.allclose(o_good, o_shift)
+
+    # swiglu backward missing the a*(1-s) term
+    a, b, g = r.standard_normal(10) * 2, r.standard_normal(10), r.standard_normal(10)
+    sg = scipy.special.expit(a)
+    da_bad = g * b * sg
+    da, _ = O.swiglu_bwd(g, a, b)
+    assert not np.allclose(da, da_bad)
