@@ -16,16 +16,29 @@
 // query's alpha is lane-uniform. P leaves the accumulator registers directly
 // as the B operand of the second product: the key order inside each
 // 16-key MFMA step is permuted identically in P^T and in the V^T fragments
-// read from LDS, which the contraction does not see. V is transposed once per
-// tile on its way into LDS (V^T rows padded to 68 keys -> 34-dword stride,
-// conflict-free 8-byte reads for 32 lanes); K rows are padded to D + 8.
+// read from LDS, which the contraction does not see.
 //
-// Softmax runs in base 2 on s * scale * log2(e); the log-sum-exp output is
-// converted back to natural log. Causal blocks only visit key tiles up to
-// their last query and a wave skips the MFMAs of a tile wholly above its
-// diagonal. Work order: longest causal rows first, and the q heads sharing a
-// kv head land on the same XCD (dispatch is round-robin over the 8 XCDs), so
-// their K/V tiles are shared through that XCD's L2.
+// LDS layouts (both conflict-free for the 8-lane b128 and 16-lane b64 phases
+// of a 32-bank LDS):
+//   K   [BN][D + 8]: row-major, rows padded by 16 bytes.
+//   V^T [D][BN + 4]: transposed on the way in. A row holds 16 four-key units;
+//       unit u of row d sits at position u ^ ((d >> 4) & 7), which spreads the
+//       transposing stores (16 lanes = 16 rows, same unit) over all banks
+//       while a read phase (16 consecutive rows, same unit) keeps one swizzle.
+// The transpose is done in registers with byte permutes (v_perm_b32).
+//
+// Keys past the end are read from the last row (clamped addresses, so no
+// load is conditional) and masked like causal ones.
+//
+// Softmax runs in base 2: raw scores s are reduced to a row max first and
+// exp2(s * c - m) is one FMA plus one exp with c = |scale| * log2(e) (a
+// negative scale negates Q on load, which is exact). The accumulator rescale
+// is skipped when no query of the wave raised its max (alpha is exactly 1).
+// The log-sum-exp output is converted back to natural log. Causal blocks only
+// visit key tiles up to their last query and a wave skips the MFMAs of a tile
+// wholly above its diagonal. Work order: longest causal rows first, and the q
+// heads sharing a kv head land on the same XCD (dispatch is round-robin over
+// the 8 XCDs), so their K/V tiles are shared through that XCD's L2.
 #include <math.h>
 
 #include "api.h"
@@ -64,8 +77,16 @@ struct AttnArgs {
   float* lse;
   int64_t qsb, qss, qsh, ksb, kss, ksh, vsb, vss, vsh, osb, oss, osh;
   int B, S, Hq, Hkv, group, m_tiles;
-  float scale_log2;
+  float c;          // |scale| * log2(e), at least 1e-30
+  uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Position of the four-key unit `u` of V^T row `d`.
+__device__ __forceinline__ int vt_unit(int d, int u) { return u ^ ((d >> 4) & 7); }
 
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_fwd_kernel(
@@ -112,75 +133,79 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const T* kbase = static_cast<const T*>(a.k) + b * a.ksb + hkv * a.ksh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.vsb + hkv * a.vsh;
 
-  // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8]
+  // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
   Frag qf[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
-    if (q_row < a.S) {
-      qf[kk] = *reinterpret_cast<const Frag*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[kk][j] = (T)0.f;
-    }
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (q_row < a.S) raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
+    raw.x ^= a.q_flip;
+    raw.y ^= a.q_flip;
+    raw.z ^= a.q_flip;
+    raw.w ^= a.q_flip;
+    qf[kk] = *reinterpret_cast<const Frag*>(&raw);
   }
 
   const int kv_end = CAUSAL ? (m0 + BM < a.S ? m0 + BM : a.S) : a.S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  // ---- tile staging
+  // ---- tile staging: K rows by 16-byte chunk; V rows V_RPT at a time for the transpose
   const int kc = tid % KCH, kr = tid / KCH;
   const int vr = (tid / KCH) * V_RPT;
   uint4 kreg[K_PASSES], vreg[V_RPT];
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  auto load_tile = [&](int t) {
-    const int kv0 = t * BN;
-#pragma unroll
-    for (int p = 0; p < K_PASSES; ++p) {
-      const int row = kv0 + kr + p * K_ROWS;
-      kreg[p] = row < a.S ? *reinterpret_cast<const uint4*>(kbase + (int64_t)row * a.kss + kc * 8) : zero4;
-    }
-#pragma unroll
-    for (int i = 0; i < V_RPT; ++i) {
-      const int row = kv0 + vr + i;
-      vreg[i] = row < a.S ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * a.vss + kc * 8) : zero4;
-    }
-  };
-  auto store_tile = [&](int buf) {
-    T* ks = Ks[buf];
-#pragma unroll
-    for (int p = 0; p < K_PASSES; ++p) *reinterpret_cast<uint4*>(ks + (kr + p * K_ROWS) * KST + kc * 8) = kreg[p];
-    T* vt = Vt[buf];
-    const unsigned short* h[V_RPT];
-#pragma unroll
-    for (int i = 0; i < V_RPT; ++i) h[i] = reinterpret_cast<const unsigned short*>(&vreg[i]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      T* dst = vt + (kc * 8 + e) * VST + vr;
-      if constexpr (V_RPT == 4) {
-        *reinterpret_cast<uint2*>(dst) =
-            make_uint2((unsigned)h[0][e] | ((unsigned)h[1][e] << 16), (unsigned)h[2][e] | ((unsigned)h[3][e] << 16));
-      } else {
-        *reinterpret_cast<unsigned*>(dst) = (unsigned)h[0][e] | ((unsigned)h[1][e] << 16);
-      }
-    }
-  };
 
-  float m_i = -INFINITY;  // running max of s*scale*log2e for query q_row
-  float l_i = 0.f;        // this lane's half of the running denominator
   f32x16 acc[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+  float m_i = -INFINITY;  // running max of s * c for query q_row
+  float l_i = 0.f;        // this lane's half of the running denominator
 
-  load_tile(0);
-  store_tile(0);
+#define PK_LOAD_TILE(t)                                                                                        \
+  do {                                                                                                         \
+    const int kv0_ = (t)*BN;                                                                                   \
+    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p) {                                                     \
+      const int row = min(kv0_ + kr + p * K_ROWS, a.S - 1);                                                    \
+      kreg[p] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * a.kss + kc * 8);                       \
+    }                                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i) {                                                        \
+      const int row = min(kv0_ + vr + i, a.S - 1);                                                             \
+      vreg[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * a.vss + kc * 8);                       \
+    }                                                                                                          \
+  } while (0)
+
+#define PK_STORE_TILE(buf)                                                                                     \
+  do {                                                                                                         \
+    T* ks_ = Ks[buf];                                                                                          \
+    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p)                                                       \
+        *reinterpret_cast<uint4*>(ks_ + (kr + p * K_ROWS) * KST + kc * 8) = kreg[p];                          \
+    T* vt_ = Vt[buf];                                                                                          \
+    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                                            \
+      const int d = kc * 8 + e;                                                                                \
+      /* low halves of word e/2 for even e, high halves for odd e */                                           \
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;                                               \
+      const uint32_t p01 = __builtin_amdgcn_perm(word(vreg[1], e >> 1), word(vreg[0], e >> 1), sel);          \
+      T* dst = vt_ + d * VST + vt_unit(d, vr >> 2) * 4 + (vr & 3);                                            \
+      if constexpr (V_RPT == 4) {                                                                              \
+        const uint32_t p23 = __builtin_amdgcn_perm(word(vreg[3], e >> 1), word(vreg[2], e >> 1), sel);        \
+        *reinterpret_cast<uint2*>(dst) = make_uint2(p01, p23);                                                 \
+      } else {                                                                                                 \
+        *reinterpret_cast<uint32_t*>(dst) = p01;                                                               \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
+
+  PK_LOAD_TILE(0);
+  PK_STORE_TILE(0);
   __syncthreads();
 
   const int wave_first = m0 + wave * 32;
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
+    // The last iteration re-reads its own tile into the idle buffer: the
+    // staging registers never sit behind a branch, which keeps them in VGPRs.
+    PK_LOAD_TILE(min(t + 1, n_tiles - 1));
     const int kv0 = t * BN;
     if (!(CAUSAL && kv0 > wave_first + 31)) {
       const T* ks = Ks[buf];
@@ -195,40 +220,46 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
           s[st] = Mma<T>::run(kf, qf[kk], s[st]);
         }
       }
-      // scale, mask, row max
+      // mask, row max of the raw scores
       const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > a.S;
+      if (need_mask) {
+        // last visible key of this lane's query; rows past the end (clamped loads) are masked too
+        const int lim = CAUSAL ? min(q_row, a.S - 1) : a.S - 1;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + st * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            s[st][r] = key <= lim ? s[st][r] : -INFINITY;
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[st][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = kv0 + st * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if ((CAUSAL && key > q_row) || key >= a.S) x = -INFINITY;
-          }
-          s[st][r] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_i, mx);
+      const float m_new = fmaxf(m_i, mx * a.c);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
       float rs = 0.f;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(s[st][r] - m_use);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][r], a.c, -m_use));
           s[st][r] = p;
           rs += p;
         }
-      l_i = l_i * alpha + rs;
+      if (!__all(m_new == m_i)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
+        l_i *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+      }
+      l_i += rs;
       m_i = m_new;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
 
       // O^T += V^T P^T, four 16-key steps
       const T* vt = Vt[buf];
@@ -239,19 +270,20 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         for (int j = 0; j < 8; ++j) pf[j] = (T)s[c >> 1][8 * (c & 1) + j];
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          const T* row = vt + (dt * 32 + r32) * VST + 16 * c + 4 * g;
-          const uint2 lo = *reinterpret_cast<const uint2*>(row);
-          const uint2 hi = *reinterpret_cast<const uint2*>(row + 8);
-          Frag vf;
-          uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          vf = *reinterpret_cast<const Frag*>(&packed);
-          acc[dt] = Mma<T>::run(vf, pf, acc[dt]);
+          const int d = dt * 32 + r32;
+          const T* row = vt + d * VST;
+          const uint2 lo = *reinterpret_cast<const uint2*>(row + vt_unit(d, 4 * c + g) * 4);
+          const uint2 hi = *reinterpret_cast<const uint2*>(row + vt_unit(d, 4 * c + 2 + g) * 4);
+          const uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          acc[dt] = Mma<T>::run(*reinterpret_cast<const Frag*>(&packed), pf, acc[dt]);
         }
       }
     }
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+    PK_STORE_TILE(buf ^ 1);
     __syncthreads();
   }
+#undef PK_LOAD_TILE
+#undef PK_STORE_TILE
 
   // ---- epilogue
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
@@ -263,10 +295,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d0 = dt * 32 + 8 * rq + 4 * g;
-        T o4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o4[i] = from_f32<T>(acc[dt][4 * rq + i] * inv);
-        *reinterpret_cast<uint2*>(orow + d0) = *reinterpret_cast<const uint2*>(o4);
+        const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq] * inv)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq + 1] * inv)) << 16);
+        const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq + 2] * inv)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq + 3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(orow + d0) = make_uint2(lo, hi);
       }
     if (a.lse != nullptr && g == 0)
       a.lse[((int64_t)b * a.Hq + hq) * a.S + q_row] = (m_i + log2f(l_tot)) * 0.69314718055994530942f;
@@ -303,6 +336,7 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
     return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: dtype code %d (bf16/fp16 only)", dtype);
   if (head_dim != 64 && head_dim != 128)
     return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: head_dim=%lld (64 or 128 only)", (long long)head_dim);
+  if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "pk_attn_fwd: softmax_scale is not finite");
   if (seq > (1 << 30) || batch * q_heads > (1 << 20))
     return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: shape too large");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
@@ -335,7 +369,8 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   a.Hkv = (int)kv_heads;
   a.group = (int)(q_heads / kv_heads);
   a.m_tiles = (int)((seq + BM - 1) / BM);
-  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
+  a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
   if ((int64_t)a.m_tiles * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: grid too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PK_BF16) return head_dim == 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
