@@ -1,0 +1,117 @@
+"""Registers the MI355X kernels as one Popcorn backend.
+
+    import popcorn, popcorn.kernels       # or: from popcorn_amd import compat as popcorn
+    from popcorn_amd import backend
+    backend.register(popcorn)
+
+This is the whole integration: one `declare_backend` (core/sources.py:40-47)
+and one `op.register(name, source=..., predicate=..., forward_only=...)` per
+op (core/dispatcher.py:324-345), exactly what a backend module under
+`popcorn/kernels/` does. Each registration is source-only: the
+`popcorn_amd.impls` functions already carry the reference signatures, so
+Popcorn calls them directly (core/dispatcher.py:184-201).
+
+The backend's distribution is `popcorn-amd` at `popcorn_amd.__version__`,
+pinned as both bounds of the version gate; its metadata sits next to the
+package (`popcorn_amd-<version>.dist-info`), so the gate resolves whenever
+the repository root is on `sys.path`, with or without a pip install.
+
+The predicates only describe what the kernels cover -- tensors on a HIP
+device, one floating dtype per call, the shapes the kernels implement.
+Anything else is declined, and Popcorn serves it with the next eligible
+implementation (the torch reference); inside the kernels an unsupported call
+raises instead of falling back.
+"""
+
+from __future__ import annotations
+
+from types import ModuleType
+from typing import Any
+
+import torch
+
+from popcorn_amd import __version__
+
+BACKEND = "mi355x"
+DISTRIBUTION = "popcorn-amd"
+
+
+def _on_hip(*tensors: Any) -> bool:
+    ts = [t for t in tensors if t is not None]
+    return (
+        torch.version.hip is not None
+        and all(isinstance(t, torch.Tensor) and t.device.type == "cuda" for t in ts)
+        and len({t.device for t in ts}) == 1
+    )
+
+
+_FLOATS = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def rms_norm_supported(x, weight, bias, eps) -> bool:
+    tensors = [t for t in (x, weight, bias) if t is not None]
+    return (
+        _on_hip(*tensors)
+        and len({t.dtype for t in tensors}) == 1
+        and x.dtype in _FLOATS
+        and x.shape[-1] > 0
+    )
+
+
+def swiglu_supported(a, b) -> bool:
+    return _on_hip(a, b) and a.dtype == b.dtype and a.dtype in _FLOATS and a.shape == b.shape
+
+
+def rotary_supported(x, cos, sin, interleaved) -> bool:
+    return (
+        _on_hip(x, cos, sin)
+        and x.dtype in _FLOATS
+        and cos.dtype in _FLOATS
+        and cos.dtype == sin.dtype
+        and x.dim() == 4
+        and 2 * cos.shape[-1] <= x.shape[-1]
+    )
+
+
+def attn_supported(q, k, v, causal, softmax_scale) -> bool:
+    return (
+        _on_hip(q, k, v)
+        and q.dtype in (torch.bfloat16, torch.float16)
+        and q.dtype == k.dtype == v.dtype
+        and q.shape[-1] in (64, 128)
+        and k.shape[2] > 0
+        and q.shape[2] % k.shape[2] == 0
+    )
+
+
+# (op, source, predicate, forward_only): attention has no backward kernel yet,
+# so Popcorn declines it whenever a call needs gradients.
+REGISTRATIONS = (
+    ("rms_norm", "popcorn_amd.impls.rms_norm", rms_norm_supported, False),
+    ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
+    ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
+    ("attn", "popcorn_amd.impls.attn", attn_supported, True),
+)
+
+
+def _popcorn() -> ModuleType:
+    try:
+        import popcorn
+        import popcorn.kernels  # noqa: F401  registers Popcorn's ops
+
+        return popcorn
+    except ImportError:
+        from popcorn_amd import compat
+
+        return compat
+
+
+def register(popcorn: ModuleType | None = None) -> ModuleType:
+    """Declare the backend and register the four ops on `popcorn` (default: the real package, else compat)."""
+    pc = popcorn if popcorn is not None else _popcorn()
+    pc.declare_backend(BACKEND, package=DISTRIBUTION, min_version=__version__, max_version=__version__)
+    for op_name, source, predicate, forward_only in REGISTRATIONS:
+        op = pc.KERNELS[op_name]
+        if BACKEND not in op.available_backends():  # registering twice is a no-op, not an error
+            op.register(BACKEND, source=source, predicate=predicate, forward_only=forward_only)
+    return pc

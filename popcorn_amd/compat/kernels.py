@@ -1,0 +1,53 @@
+"""The four transformer-block ops, registered with their torch references.
+
+Signatures, shape annotations and test-argument pools are Popcorn's
+(kernels/rms_norm.py:16-30, kernels/swiglu.py:9-18,
+kernels/rotary_embedding.py:12-40, kernels/attn.py:10-37); the arithmetic is
+the eager-torch restatement in `popcorn_amd.compat.references`.
+"""
+
+from torch import Tensor
+
+from popcorn_amd.compat import references
+from popcorn_amd.compat.dispatcher import register_kernel
+from popcorn_amd.compat.shapes import Float
+
+
+@register_kernel(test_args={"eps": [1e-6, 1e-5]})
+def rms_norm(
+    x: Float[Tensor, "... normalized_shape"],
+    weight: Float[Tensor, "normalized_shape"],
+    bias: Float[Tensor, "normalized_shape"] | None = None,
+    eps: float = 1e-6,
+) -> Float[Tensor, "... normalized_shape"]:
+    """Root-mean-square normalization: x * rsqrt(mean(x^2) + eps) * weight (+ bias)."""
+    return references.rms_norm(x, weight, bias, eps)
+
+
+@register_kernel
+def swiglu(a: Float[Tensor, "... hidden"], b: Float[Tensor, "... hidden"]) -> Float[Tensor, "... hidden"]:
+    """SwiGLU gating: silu(a) * b."""
+    return references.swiglu(a, b)
+
+
+@register_kernel
+def rotary_embedding(
+    x: Float[Tensor, "batch seq heads head_dim"],
+    cos: Float[Tensor, "seq half"],
+    sin: Float[Tensor, "seq half"],
+    interleaved: bool = False,
+) -> Float[Tensor, "batch seq heads head_dim"]:
+    """Rotary position embedding, GPT-NeoX halves or GPT-J interleaved pairs."""
+    return references.rotary_embedding(x, cos, sin, interleaved)
+
+
+@register_kernel(test_args={"softmax_scale": [None, 0.25]})
+def attn(
+    q: Float[Tensor, "batch seq q_heads head_dim"],
+    k: Float[Tensor, "batch seq kv_heads head_dim"],
+    v: Float[Tensor, "batch seq kv_heads head_dim"],
+    causal: bool = False,
+    softmax_scale: float | None = None,
+) -> Float[Tensor, "batch seq q_heads head_dim"]:
+    """Multi-head attention with grouped kv heads (q_heads a multiple of kv_heads)."""
+    return references.attn(q, k, v, causal, softmax_scale)

@@ -58,7 +58,35 @@ def rotary_embedding(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = Fa
 
 
 def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None) -> Tensor:
-    """torch SDPA on head-major views, grouped kv heads, returned in [batch, seq, heads, dim]."""
-    heads_first = [t.transpose(1, 2) for t in (q, k, v)]
-    out = F.scaled_dot_product_attention(*heads_first, scale=softmax_scale, is_causal=causal, enable_gqa=True)
+    """softmax(q k^T * scale + causal mask) v with grouped kv heads, in [batch, seq, heads, dim].
+
+    On the CPU this is Popcorn's own call: SDPA on head-major views with
+    enable_gqa=True. On a HIP device the same function is evaluated without
+    torch's batched products on transposed views (their 16-bit form has
+    faulted MI355X boxes): kv heads are repeated per group (SDPA's
+    enable_gqa grouping, q head h reads kv head h // group), 16-bit inputs
+    go to the fused flash / memory-efficient SDPA kernels, and fp32 / fp64
+    inputs take an explicit softmax over products of contiguous operands.
+    """
+    if q.device.type != "cuda":
+        heads_first = [t.transpose(1, 2) for t in (q, k, v)]
+        out = F.scaled_dot_product_attention(*heads_first, scale=softmax_scale, is_causal=causal, enable_gqa=True)
+        return out.transpose(1, 2)
+    group = q.shape[2] // k.shape[2]
+    qh = q.transpose(1, 2).contiguous()
+    kh = k.repeat_interleave(group, dim=2).transpose(1, 2).contiguous()
+    vh = v.repeat_interleave(group, dim=2).transpose(1, 2).contiguous()
+    scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
+    if q.dtype in (torch.float16, torch.bfloat16):
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            out = F.scaled_dot_product_attention(qh, kh, vh, scale=scale, is_causal=causal)
+        return out.transpose(1, 2)
+    scores = torch.matmul(qh, kh.transpose(-2, -1).contiguous()) * scale
+    if causal:
+        seq_q, seq_k = scores.shape[-2], scores.shape[-1]
+        mask = torch.ones(seq_q, seq_k, dtype=torch.bool, device=q.device).triu(1)
+        scores = scores.masked_fill(mask, float("-inf"))
+    out = torch.matmul(torch.softmax(scores, dim=-1), vh)
     return out.transpose(1, 2)

@@ -1,0 +1,69 @@
+"""The C ABI library loads and exports every entry point include/popcorn_amd.h declares.
+
+Only argument validation is exercised here: those paths return before any
+HIP call, so they run without a GPU. Compute calls are the GPU tests' job.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from popcorn_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "popcorn_amd.h"
+
+
+def declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(pk_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIBRARY.exists():
+        pytest.fail(f"{_lib.LIBRARY} is not built; run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    names = declared()
+    assert names, "no pk_* declarations found"
+    assert names == set(_lib.SIGNATURES), "ctypes bindings and the header disagree"
+    raw = ctypes.CDLL(str(_lib.LIBRARY))
+    for name in names:
+        assert hasattr(raw, name), f"{name} is declared but not exported"
+
+
+def test_version_and_status_codes(lib):
+    assert lib.pk_version() == _lib.ABI_VERSION
+    text = HEADER.read_text()
+    for name, value in (("PK_OK", _lib.OK), ("PK_ERR_INVALID", _lib.ERR_INVALID),
+                        ("PK_ERR_UNSUPPORTED", _lib.ERR_UNSUPPORTED), ("PK_ERR_HIP", _lib.ERR_HIP),
+                        ("PK_F32", _lib.F32), ("PK_BF16", _lib.BF16), ("PK_F16", _lib.F16)):
+        assert re.search(rf"#define {name} {value}\b", text), name
+
+
+def test_invalid_arguments_are_rejected_before_any_launch(lib):
+    assert lib.pk_swiglu_fwd(None, None, None, -1, _lib.BF16, None) == _lib.ERR_INVALID
+    assert "negative size" in lib.pk_last_error().decode()
+    assert lib.pk_swiglu_fwd(None, None, None, 0, _lib.BF16, None) == _lib.OK  # empty: nothing to do
+    assert lib.pk_swiglu_fwd(None, None, None, 8, 7, None) in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED)
+    assert lib.pk_rmsnorm_fwd(None, None, None, None, None, -1, 8, 1e-6, _lib.F32, None) == _lib.ERR_INVALID
+    assert lib.pk_rmsnorm_bwd_workspace(0, 8, _lib.BF16) == 0
+    assert lib.pk_rmsnorm_bwd_workspace(4096, 8192, _lib.BF16) > 0
+    strides = (ctypes.c_int64 * 12)(*([8] * 12))
+    rc = lib.pk_attn_fwd(None, None, None, None, None, strides, 1, 16, 4, 3, 64, 0.125, 1, _lib.BF16, None)
+    assert rc == _lib.ERR_INVALID  # null pointers
+    rot = (ctypes.c_int64 * 6)(*([128] * 6))
+    rc = lib.pk_rotary(None, None, None, None, rot, 1, 4, 2, 128, 80, _lib.BF16, _lib.F32, 0, 0, None)
+    assert rc == _lib.ERR_INVALID and "half" in lib.pk_last_error().decode()
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "absent.so")

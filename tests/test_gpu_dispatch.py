@@ -1,0 +1,126 @@
+"""The backend through Popcorn's register -> validate -> record -> select path, on an MI355X.
+
+`op.benchmark(..., backend="mi355x")` runs the harness (float64 truth,
+native-dtype budget, timings) and writes a schema-3 row to the user cache;
+a plain `op(...)` afterwards must route to the backend exactly when its
+recorded time beats torch's by more than the 3% indifference margin
+(core/policy.py:30, 164-172). Reference-side attention is evaluated through
+fused SDPA kernels or explicit contiguous products (compat.references.attn).
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+from popcorn_amd import backend, compat, impls
+from popcorn_amd.compat import store
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAME = backend.BACKEND
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _registered():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    backend.register(compat)
+
+
+@pytest.fixture(autouse=True)
+def _fresh_selection(tmp_path, monkeypatch):
+    monkeypatch.setattr(store, "BUNDLED_REPORTS", tmp_path / "bundled")
+    for op in compat.KERNELS.values():
+        op.tuner.forget()
+    yield
+    for op in compat.KERNELS.values():
+        op.tuner.forget()
+
+
+def _randn(*shape, dtype=torch.bfloat16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype).to(DEV)
+
+
+def _selected(op):
+    assert op.tuner._selected, "no selection was made"
+    return list(op.tuner._selected.values())[-1].name
+
+
+def _check_record_and_route(op, record, call):
+    r = record.result
+    assert record.impl == NAME and r.status == "pass", (r.status, r.reason)
+    assert r.benchmarked and r.bench["fwd_ms"] > 0 and r.bench["ref_fwd_ms"] > 0, r.bench_error
+    ours = r.bench["fwd_ms"] + r.bench.get("bwd_ms", 0.0)
+    theirs = r.bench["ref_fwd_ms"] + r.bench.get("ref_bwd_ms", 0.0)
+    print(f"{op.name}: {NAME} {ours:.4f} ms vs torch {theirs:.4f} ms ({theirs / ours:.1f}x)", flush=True)
+    op.tuner.forget()
+    call()
+    expect = NAME if ours * 1.03 < theirs else "torch"
+    assert _selected(op) == expect
+    rows = [json.loads(line) for line in (store.user_reports() / f"{op.name}.jsonl").read_text().splitlines()]
+    assert any(row["impl"] == NAME and row["status"] == "pass" for row in rows)
+
+
+def test_rms_norm_records_and_routes_with_grad():
+    op = compat.KERNELS["rms_norm"]
+    x = _randn(4096, 4096).requires_grad_()
+    w = (1 + 0.1 * _randn(4096, dtype=torch.float32, seed=1)).bfloat16().requires_grad_()
+    [record] = op.benchmark(x, w, backend=NAME)
+    assert record.result.grad and "x" in record.result.bwd and "weight" in record.result.bwd
+    _check_record_and_route(op, record, lambda: op(x, w))
+
+
+def test_swiglu_records_and_routes_with_grad():
+    op = compat.KERNELS["swiglu"]
+    a, b = _randn(4096, 8192).requires_grad_(), _randn(4096, 8192, seed=1).requires_grad_()
+    [record] = op.benchmark(a, b, backend=NAME)
+    _check_record_and_route(op, record, lambda: op(a, b))
+
+
+def test_rotary_records_and_routes():
+    op = compat.KERNELS["rotary_embedding"]
+    x = _randn(4, 1024, 16, 128).requires_grad_()
+    cos, sin = _randn(1024, 64, seed=1), _randn(1024, 64, seed=2)  # the harness's all-bf16 randn tables
+    [record] = op.benchmark(x, cos, sin, backend=NAME)
+    _check_record_and_route(op, record, lambda: op(x, cos, sin))
+
+
+def test_attn_forward_only_records_and_routes():
+    op = compat.KERNELS["attn"]
+    q, k, v = _randn(1, 1024, 8, 128), _randn(1, 1024, 2, 128, seed=1), _randn(1, 1024, 2, 128, seed=2)
+    with torch.no_grad():
+        [record] = op.benchmark(q, k, v, True, backend=NAME)
+        assert not record.result.grad
+        _check_record_and_route(op, record, lambda: op(q, k, v, True))
+    # a call that needs gradients is declined by the forward-only backend
+    qg = q.clone().requires_grad_()
+    op.tuner.forget()
+    op(qg, k, v, True)
+    assert _selected(op) == "torch"
+
+
+def test_mixed_dtype_rotary_is_served_in_registration_order():
+    """bf16 x with fp32 tables has no single dtype, so no record applies (core/config.py:95-99)."""
+    op = compat.KERNELS["rotary_embedding"]
+    x = _randn(2, 64, 4, 128)
+    pos = torch.arange(64, dtype=torch.float64, device=DEV)[:, None]
+    ang = pos * 500000.0 ** (-torch.arange(64, dtype=torch.float64, device=DEV) / 64)
+    cos, sin = ang.cos().float(), ang.sin().float()
+    y = op(x, cos, sin)
+    assert _selected(op) == NAME
+    assert torch.equal(y, impls.rotary_embedding(x, cos, sin))
+
+
+def test_bench_mode_measures_lazily(monkeypatch):
+    op = compat.KERNELS["swiglu"]
+    monkeypatch.setenv("POPCORN_BENCH", "1")
+    a, b = _randn(512, 4096), _randn(512, 4096, seed=1)
+    op(a, b)
+    rows = [json.loads(line) for line in (store.user_reports() / "swiglu.jsonl").read_text().splitlines()]
+    assert [(r["impl"], r["status"], r["benchmarked"]) for r in rows] == [(NAME, "pass", True)]
+    op(a, b)  # already measured: no new row
+    assert len((store.user_reports() / "swiglu.jsonl").read_text().splitlines()) == 1
