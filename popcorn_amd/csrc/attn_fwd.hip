@@ -2,8 +2,9 @@
 // gfx950 matrix cores.
 //
 // Block = 4 wavefronts x 32 query rows (BM = 128) of one (batch, q head);
-// keys stream through LDS in tiles of BN = 64, double-buffered: the global
-// loads of tile t+1 are in flight while tile t is multiplied.
+// keys stream through LDS in tiles of BN = 64, double-buffered: K and V of
+// tile t+1 are fetched into registers (buffer loads) while tile t is
+// multiplied, then stored to the idle LDS buffer.
 //
 // Per tile each wave computes
 //   S^T (32 keys x 32 queries)  = K_tile . Q^T   (v_mfma_f32_32x32x16, K from
@@ -15,30 +16,33 @@
 // except for one exchange with lane l^32, and the rescale of O^T by that
 // query's alpha is lane-uniform. P leaves the accumulator registers directly
 // as the B operand of the second product: the key order inside each
-// 16-key MFMA step is permuted identically in P^T and in the V^T fragments
-// read from LDS, which the contraction does not see.
+// 16-key MFMA step is permuted identically in P^T and in the V^T fragments,
+// which the contraction does not see.
 //
-// LDS layouts (both conflict-free for the 8-lane b128 and 16-lane b64 phases
-// of a 32-bank LDS):
-//   K   [BN][D + 8]: row-major, rows padded by 16 bytes.
-//   V^T [D][BN + 4]: transposed on the way in. A row holds 16 four-key units;
-//       unit u of row d sits at position u ^ ((d >> 4) & 7), which spreads the
-//       transposing stores (16 lanes = 16 rows, same unit) over all banks
-//       while a read phase (16 consecutive rows, same unit) keeps one swizzle.
-// The transpose is done in registers with byte permutes (v_perm_b32).
+// LDS layouts:
+//   K [BN][D]: 16-byte chunk c of row r sits at chunk position c ^ (r % (D/8)),
+//       so the 16-byte fragment reads of consecutive rows hit distinct banks.
+//   V [BN][D + 16]: row-major. V^T fragments come from ds_read_b64_tr_b16:
+//       within a 16-lane group, lane s reads keys base + s/4, dims
+//       d0 + 4*(s%4) .. +3, and lane i receives dims d0 + i of keys
+//       base .. base + 3 -- half of one MFMA A fragment; the padding puts the
+//       four rows of one read on different banks.
 //
-// Keys past the end are read from the last row (clamped addresses, so no
-// load is conditional) and masked like causal ones.
+// K and V are read through buffer resources based at the (batch, kv head):
+// a tile is one scalar offset, and rows at or past S read as zero, so no load
+// is predicated; such keys are masked like causal ones.
 //
 // Softmax runs in base 2: raw scores s are reduced to a row max first and
 // exp2(s * c - m) is one FMA plus one exp with c = |scale| * log2(e) (a
-// negative scale negates Q on load, which is exact). The accumulator rescale
-// is skipped when no query of the wave raised its max (alpha is exactly 1).
-// The log-sum-exp output is converted back to natural log. Causal blocks only
-// visit key tiles up to their last query and a wave skips the MFMAs of a tile
-// wholly above its diagonal. Work order: longest causal rows first, and the q
-// heads sharing a kv head land on the same XCD (dispatch is round-robin over
-// the 8 XCDs), so their K/V tiles are shared through that XCD's L2.
+// negative scale negates Q on load, which is exact). The running max m only
+// moves when some query's candidate exceeds it by more than 8: exponents stay
+// <= 8, and o = acc / l uses the same m in both, so the result is unchanged
+// while most tiles skip the O rescale. The log-sum-exp output is converted
+// back to natural log. Causal blocks only visit key tiles up to their last
+// query and a wave skips the MFMAs of a tile wholly above its diagonal. Work
+// order: longest causal rows first, and the q heads sharing a kv head land on
+// the same XCD (dispatch is round-robin over the 8 XCDs), so their K/V tiles
+// are shared through that XCD's L2.
 #include <math.h>
 
 #include "api.h"
@@ -77,30 +81,33 @@ struct AttnArgs {
   float* lse;
   int64_t qsb, qss, qsh, ksb, kss, ksh, vsb, vss, vsh, osb, oss, osh;
   int B, S, Hq, Hkv, group, m_tiles;
+  int k_bytes, v_bytes;  // bytes from a (batch, kv head) base to the end of its last row
   float c;          // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
 
-__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s4;
 
-// Position of the four-key unit `u` of V^T row `d`.
-__device__ __forceinline__ int vt_unit(int d, int u) { return u ^ ((d >> 4) & 7); }
+__device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_fwd_kernel(
     AttnArgs a) {
   using Frag = typename Mma<T>::frag;
-  constexpr int KST = D + 8;   // K row stride in LDS, elements
-  constexpr int VST = BN + 4;  // V^T row stride in LDS, elements
+  constexpr int KST = D;       // K row stride in LDS, elements (16-byte chunks XOR-swizzled by row)
+  constexpr int VST = D + 16;  // V row stride in LDS, elements (row-major; read transposed)
   constexpr int KCH = D / 8;   // 16-byte chunks per K/V row
   constexpr int K_ROWS = NT / KCH;
   constexpr int K_PASSES = BN / K_ROWS;
   constexpr int V_RPT = BN * KCH / NT;  // consecutive V rows per thread
-  static_assert(V_RPT == 2 || V_RPT == 4, "V transpose packs 2 or 4 keys");
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
-  __shared__ __attribute__((aligned(16))) T Vt[2][D * VST];
+  __shared__ __attribute__((aligned(16))) T Vs[2][BN * VST];
 
   // ---- work item: (batch, kv head, q tile) groups, q heads of a group adjacent on one XCD
   const int G = a.group;
@@ -132,6 +139,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const T* qbase = static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh;
   const T* kbase = static_cast<const T*>(a.k) + b * a.ksb + hkv * a.ksh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.vsb + hkv * a.vsh;
+  // K/V of this (batch, kv head) through buffer resources: rows at or past S
+  // read as zero (range-checked), and a tile's base is one scalar offset.
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, a.k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, a.v_bytes, 0x00020000);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
   Frag qf[D / 16];
@@ -149,10 +162,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int kv_end = CAUSAL ? (m0 + BM < a.S ? m0 + BM : a.S) : a.S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  // ---- tile staging: K rows by 16-byte chunk; V rows V_RPT at a time for the transpose
+  // ---- tile staging: K rows by 16-byte chunk, V rows V_RPT at a time
   const int kc = tid % KCH, kr = tid / KCH;
   const int vr = (tid / KCH) * V_RPT;
+  const int koff = (kr * (int)a.kss + kc * 8) * (int)sizeof(T);  // byte offset of this lane's first K chunk
+  const int voff = (vr * (int)a.vss + kc * 8) * (int)sizeof(T);
   uint4 kreg[K_PASSES], vreg[V_RPT];
+  // this lane's element offsets of its K fragments (row r32, chunk 2kk + g, swizzled)
+  int k_lane[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) k_lane[kk] = r32 * KST + (((2 * kk + g) ^ (r32 & (KCH - 1))) * 8);
+  // this lane's element offset for the transposing V reads (see the PV loop)
+  const int v_lane = (4 * g + ((lane & 15) >> 2)) * VST + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -164,36 +185,22 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 #define PK_LOAD_TILE(t)                                                                                        \
   do {                                                                                                         \
-    const int kv0_ = (t)*BN;                                                                                   \
-    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p) {                                                     \
-      const int row = min(kv0_ + kr + p * K_ROWS, a.S - 1);                                                    \
-      kreg[p] = *reinterpret_cast<const uint4*>(kbase + (int64_t)row * a.kss + kc * 8);                       \
-    }                                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i) {                                                        \
-      const int row = min(kv0_ + vr + i, a.S - 1);                                                             \
-      vreg[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * a.vss + kc * 8);                       \
-    }                                                                                                          \
+    const int ktile_ = (t)*BN * (int)a.kss * (int)sizeof(T);                                                   \
+    const int vtile_ = (t)*BN * (int)a.vss * (int)sizeof(T);                                                   \
+    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p)                                                       \
+      kreg[p] = ld_buf(krsrc, koff + p * K_ROWS * (int)a.kss * (int)sizeof(T), ktile_);                       \
+    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i)                                                          \
+      vreg[i] = ld_buf(vrsrc, voff + i * (int)a.vss * (int)sizeof(T), vtile_);                                \
   } while (0)
 
 #define PK_STORE_TILE(buf)                                                                                     \
   do {                                                                                                         \
     T* ks_ = Ks[buf];                                                                                          \
     _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p)                                                       \
-        *reinterpret_cast<uint4*>(ks_ + (kr + p * K_ROWS) * KST + kc * 8) = kreg[p];                          \
-    T* vt_ = Vt[buf];                                                                                          \
-    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                                            \
-      const int d = kc * 8 + e;                                                                                \
-      /* low halves of word e/2 for even e, high halves for odd e */                                           \
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;                                               \
-      const uint32_t p01 = __builtin_amdgcn_perm(word(vreg[1], e >> 1), word(vreg[0], e >> 1), sel);          \
-      T* dst = vt_ + d * VST + vt_unit(d, vr >> 2) * 4 + (vr & 3);                                            \
-      if constexpr (V_RPT == 4) {                                                                              \
-        const uint32_t p23 = __builtin_amdgcn_perm(word(vreg[3], e >> 1), word(vreg[2], e >> 1), sel);        \
-        *reinterpret_cast<uint2*>(dst) = make_uint2(p01, p23);                                                 \
-      } else {                                                                                                 \
-        *reinterpret_cast<uint32_t*>(dst) = p01;                                                               \
-      }                                                                                                        \
-    }                                                                                                          \
+        *reinterpret_cast<uint4*>(ks_ + (kr + p * K_ROWS) * KST + (kc ^ ((kr + p * K_ROWS) & (KCH - 1))) * 8) = kreg[p]; \
+    T* vs_ = Vs[buf];                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i)                                                          \
+        *reinterpret_cast<uint4*>(vs_ + (vr + i) * VST + kc * 8) = vreg[i];                                   \
   } while (0)
 
   PK_LOAD_TILE(0);
@@ -216,7 +223,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         for (int r = 0; r < 16; ++r) s[st][r] = 0.f;
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-          const Frag kf = *reinterpret_cast<const Frag*>(ks + (st * 32 + r32) * KST + 16 * kk + 8 * g);
+          const Frag kf = *reinterpret_cast<const Frag*>(ks + st * 32 * KST + k_lane[kk]);
           s[st] = Mma<T>::run(kf, qf[kk], s[st]);
         }
       }
@@ -239,8 +246,22 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_i, mx * a.c);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      // The running max only moves when some query's max grew by more than
+      // 2^8: exponents then stay <= 8 (p <= 256, exact in bf16 range) and the
+      // final o = acc / l uses the same stale max in both, so the result is
+      // unchanged while most tiles skip the O rescale entirely.
+      const float m_cand = mx * a.c;
+      if (!__all(m_cand <= m_i + 8.0f)) {
+        const float m_new = fmaxf(m_i, m_cand);
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);  // 0 when m_i = -inf
+        l_i *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+        m_i = m_new;
+      }
+      const float m_use = m_i == -INFINITY ? 0.f : m_i;
       float rs = 0.f;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -250,19 +271,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
           s[st][r] = p;
           rs += p;
         }
-      if (!__all(m_new == m_i)) {
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_use);
-        l_i *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-      }
       l_i += rs;
-      m_i = m_new;
 
       // O^T += V^T P^T, four 16-key steps
-      const T* vt = Vt[buf];
+      // V^T fragments by transposing reads of row-major V: within each 16-lane
+      // group, lane s reads keys (base + s/4), dims (d0 + 4*(s%4)) .. +3, and
+      // lane i receives dims d0 + i of keys base .. base + 3.
+      lds_s4* vt = (lds_s4*)(Vs[buf] + v_lane);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         Frag pf;
@@ -270,12 +285,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         for (int j = 0; j < 8; ++j) pf[j] = (T)s[c >> 1][8 * (c & 1) + j];
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          const int d = dt * 32 + r32;
-          const T* row = vt + d * VST;
-          const uint2 lo = *reinterpret_cast<const uint2*>(row + vt_unit(d, 4 * c + g) * 4);
-          const uint2 hi = *reinterpret_cast<const uint2*>(row + vt_unit(d, 4 * c + 2 + g) * 4);
-          const uint4 packed = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[dt] = Mma<T>::run(*reinterpret_cast<const Frag*>(&packed), pf, acc[dt]);
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
+          const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, both), pf, acc[dt]);
         }
       }
     }
@@ -369,6 +382,12 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   a.Hkv = (int)kv_heads;
   a.group = (int)(q_heads / kv_heads);
   a.m_tiles = (int)((seq + BM - 1) / BM);
+  // buffer offsets are 32-bit: every row offset inside one (batch, kv head) must fit
+  const int64_t k_span = ((seq - 1) * strides[4] + head_dim) * 2, v_span = ((seq - 1) * strides[7] + head_dim) * 2;
+  if (k_span > INT32_MAX - 4096 || v_span > INT32_MAX - 4096)
+    return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: K/V rows span more than 2 GiB per head");
+  a.k_bytes = (int)k_span;
+  a.v_bytes = (int)v_span;
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
   if ((int64_t)a.m_tiles * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: grid too large");
