@@ -15,6 +15,9 @@ int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)))
 // Converts the launch status of the kernels just enqueued into a C-ABI status.
 int launched(const char* what);
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+int cu_count();
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int elem_size(int dtype) { return dtype == PK_F32 ? 4 : 2; }

@@ -1,44 +1,46 @@
 // RMSNorm forward and backward: row passes that read each operand from HBM
 // once.
 //
-// Fast path (cols a multiple of the 16-byte pack and at most 256*8 packs):
-// a row is held in registers by TPR lanes (64 = one wavefront per row, or 256
-// = the whole 4-wave block), each lane owning VPT packs strided by TPR so a
-// wave's loads are contiguous. The sum of squares is a DPP/shuffle wave
-// reduction plus, for TPR=256, a 4-entry LDS exchange. Any other shape takes
+// Fast path (cols a multiple of the 16-byte pack, at most 1024*16 packs): a
+// row is held in registers by TPR lanes, each owning VPT packs strided by TPR
+// so a wave's loads are contiguous. TPR = 64 is one wavefront per row (several
+// rows per block, sum of squares by wave shuffles alone); TPR = NTB is the
+// whole block (a wave reduction plus one LDS exchange). Any other shape takes
 // a one-block-per-row kernel that loops over the row twice.
 //
-// Backward keeps w and the running dw / dbias columns in registers for a
-// block that walks a contiguous run of rows, prefetching the next row's x and
-// dy while the current row's dot product is reduced. Per-block fp32 partial
-// rows go to a workspace and one more kernel sums them in a fixed order, so dw
-// is deterministic.
+// Backward is a persistent grid (a few blocks per CU): each block walks a
+// contiguous run of rows with w and its running dw / dbias columns in
+// registers, prefetching the next row's x and dy while the current row's dot
+// product is reduced. Blocks leave one fp32 partial row each (the rows of a
+// block's wavefront slots are combined through LDS first), and a two-stage
+// column reduction sums the partials in a fixed order, so dw is
+// deterministic.
 #include "api.h"
 #include "common.h"
 
 namespace pk {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-constexpr int kMaxVpt = 8;
-constexpr int kBwdMaxBlocks = 1024;
+constexpr int kThreads = 256;    // fallback kernels and column sums
+constexpr int kMaxVpt = 16;
+constexpr int kColSplit = 32;    // partial rows summed per block in the first column-sum stage
 
-// Sum over the TPR lanes that share a row. TPR=64: one wave. TPR=256: the
-// block; `red` holds one slot per wave and the call is a block barrier.
-template <int TPR> __device__ __forceinline__ float row_sum(float v, float* red) {
+// Sum over the TPR lanes that share a row: TPR = 64 is one wave; TPR = NTB is
+// the block, `red` holds one slot per wave and the call is a block barrier.
+template <int NTB, int TPR> __device__ __forceinline__ float row_sum(float v, float* red) {
   v = wave_sum(v);
   if constexpr (TPR == 64) {
     return v;
   } else {
-    static_assert(TPR == kThreads, "rows span one wave or the whole block");
+    static_assert(TPR == NTB, "rows span one wave or the whole block");
+    constexpr int W = NTB / 64;
     const int wave = threadIdx.x / 64;
     __syncthreads();  // previous readers of `red` are done
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
     float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) t += red[i];
+    for (int i = 0; i < W; ++i) t += red[i];
     return t;
   }
 }
@@ -50,14 +52,16 @@ template <typename T, bool BIAS> __device__ __forceinline__ T fwd_elem(float xv,
   return from_f32<T>(y);
 }
 
-template <typename T, int TPR, int VPT, bool BIAS>
-__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(const T* __restrict__ x, const T* __restrict__ w,
-                                                            const T* __restrict__ bias, T* __restrict__ y,
-                                                            float* __restrict__ rstd, int64_t rows, int cols,
-                                                            float eps, float inv_cols) {
+// One row per TPR lanes, RPB = NTB / TPR rows per block. (A persistent
+// variant keeping w in registers measured slower on MI355X.)
+template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+__global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, const T* __restrict__ w,
+                                                       const T* __restrict__ bias, T* __restrict__ y,
+                                                       float* __restrict__ rstd, int64_t rows, int cols, float eps,
+                                                       float inv_cols) {
   constexpr int P = Vec<T>::N;
-  constexpr int RPB = kThreads / TPR;
-  __shared__ float red[kWaves];
+  constexpr int RPB = NTB / TPR;
+  __shared__ float red[NTB / 64];
   const int lane = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
   const bool live = row < rows;
@@ -78,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(const T* __restrict_
       }
     }
   }
-  ss = row_sum<TPR>(ss, red);
+  ss = row_sum<NTB, TPR>(ss, red);
   if (!live) return;
   const float r = 1.0f / sqrtf(ss * inv_cols + eps);
   if (rstd != nullptr && lane == 0) rstd[row] = r;
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict_
                                                             const T* __restrict__ bias, T* __restrict__ y,
                                                             float* __restrict__ rstd, int64_t rows, int cols,
                                                             float eps, float inv_cols) {
-  __shared__ float red[kWaves];
+  __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
   float ss = 0.f;
@@ -114,7 +118,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict_
     const float f = to_f32(xr[c]);
     ss += f * f;
   }
-  ss = row_sum<kThreads>(ss, red);
+  ss = row_sum<kThreads, kThreads>(ss, red);
   const float r = 1.0f / sqrtf(ss * inv_cols + eps);
   if (rstd != nullptr && threadIdx.x == 0) rstd[row] = r;
   T* yr = y + row * cols;
@@ -125,16 +129,59 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict_
 // ---------------------------------------------------------------------------
 // backward
 
-template <typename T, int TPR, int VPT, bool BIAS>
-__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(const T* __restrict__ x, const T* __restrict__ w,
-                                                            const float* __restrict__ rstd,
-                                                            const T* __restrict__ dy, T* __restrict__ dx,
-                                                            float* __restrict__ dw_part,
-                                                            float* __restrict__ db_part, int64_t rows, int cols,
-                                                            float inv_cols, int64_t rows_per_block) {
+// Adds this lane's VPT*P column values into the block's partial row in LDS
+// (slot by slot, so the order is fixed) and lets slot 0 write it out.
+template <int NTB, int TPR, int VPT, int P>
+__device__ __forceinline__ void flush_partial(float (&acc)[VPT][P], float* lds_row, float* __restrict__ dst,
+                                              int nvec) {
+  constexpr int RPB = NTB / TPR;
+  const int lane = threadIdx.x % TPR;
+  const int slot = threadIdx.x / TPR;
+  if constexpr (RPB > 1) {
+    for (int s = RPB - 1; s >= 1; --s) {
+      if (slot == s) {
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+          const int v = lane + k * TPR;
+          if (v < nvec)
+#pragma unroll
+            for (int j = 0; j < P; ++j) lds_row[v * P + j] = (s == RPB - 1 ? 0.f : lds_row[v * P + j]) + acc[k][j];
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int v = lane + k * TPR;
+      if (v < nvec) {
+#pragma unroll
+        for (int j = 0; j < P; j += 4) {
+          float4 o = make_float4(acc[k][j], acc[k][j + 1], acc[k][j + 2], acc[k][j + 3]);
+          if constexpr (RPB > 1) {
+            o.x += lds_row[v * P + j];
+            o.y += lds_row[v * P + j + 1];
+            o.z += lds_row[v * P + j + 2];
+            o.w += lds_row[v * P + j + 3];
+          }
+          *reinterpret_cast<float4*>(dst + v * P + j) = o;
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+__global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, const T* __restrict__ w,
+                                                       const float* __restrict__ rstd, const T* __restrict__ dy,
+                                                       T* __restrict__ dx, float* __restrict__ dw_part,
+                                                       float* __restrict__ db_part, int64_t rows, int cols,
+                                                       float inv_cols, int64_t rows_per_block) {
   constexpr int P = Vec<T>::N;
-  constexpr int RPB = kThreads / TPR;
-  __shared__ float red[kWaves];
+  constexpr int RPB = NTB / TPR;
+  __shared__ float red[NTB / 64];
+  extern __shared__ float lds_row[];  // cols floats when RPB > 1
   const int lane = threadIdx.x % TPR;
   const int slot = threadIdx.x / TPR;
   const int nvec = cols / P;
@@ -156,8 +203,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(const T* __restrict_
   // This block owns rows [row0, row_end); slot s takes row0 + s, + RPB, ...
   const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t row_end = row0 + rows_per_block < rows ? row0 + rows_per_block : rows;
-  // Every slot runs the same trip count so the TPR=256 barriers line up.
-  const int64_t trips = (row_end - row0 + RPB - 1) / RPB;
+  // Every slot runs the same trip count so block-wide barriers line up.
+  const int64_t trips = row_end > row0 ? (row_end - row0 + RPB - 1) / RPB : 0;
 
   Vec<T> xv[VPT], gv[VPT], xn[VPT], gn[VPT];
   auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* go) {
@@ -186,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(const T* __restrict_
         for (int j = 0; j < P; ++j) dot += to_f32(gv[k].v[j]) * wf[k][j] * (to_f32(xv[k].v[j]) * r);
       }
     }
-    dot = row_sum<TPR>(dot, red) * inv_cols;
+    dot = row_sum<NTB, TPR>(dot, red) * inv_cols;
     if (live) {
 #pragma unroll
       for (int k = 0; k < VPT; ++k) {
@@ -212,29 +259,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(const T* __restrict_
     }
   }
 
-  // One partial row per (block, slot).
-  const int64_t prow = (int64_t)blockIdx.x * RPB + slot;
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int v = lane + k * TPR;
-    if (v < nvec) {
-      float* dst = dw_part + prow * cols + v * P;
-#pragma unroll
-      for (int j = 0; j < P; j += 4)
-        *reinterpret_cast<float4*>(dst + j) = make_float4(dwa[k][j], dwa[k][j + 1], dwa[k][j + 2], dwa[k][j + 3]);
-      if constexpr (BIAS) {
-        float* bdst = db_part + prow * cols + v * P;
-#pragma unroll
-        for (int j = 0; j < P; j += 4)
-          *reinterpret_cast<float4*>(bdst + j) =
-              make_float4(dba[k][j], dba[k][j + 1], dba[k][j + 2], dba[k][j + 3]);
-      }
-    }
+  flush_partial<NTB, TPR, VPT, P>(dwa, lds_row, dw_part + (int64_t)blockIdx.x * cols, nvec);
+  if constexpr (BIAS) {
+    if constexpr (RPB > 1) __syncthreads();  // lds_row is reused
+    flush_partial<NTB, TPR, VPT, P>(dba, lds_row, db_part + (int64_t)blockIdx.x * cols, nvec);
   }
 }
 
 // Any row width: one block walks rows_per_block rows, one column per thread
-// per step, partial rows as above (one per block).
+// per step, one partial row per block.
 template <typename T, bool BIAS>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict__ x, const T* __restrict__ w,
                                                             const float* __restrict__ rstd,
@@ -242,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
                                                             float* __restrict__ dw_part,
                                                             float* __restrict__ db_part, int64_t rows, int cols,
                                                             float inv_cols, int64_t rows_per_block) {
-  __shared__ float red[kWaves];
+  __shared__ float red[kThreads / 64];
   const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t row_end = row0 + rows_per_block < rows ? row0 + rows_per_block : rows;
   float* dwp = dw_part + (int64_t)blockIdx.x * cols;
@@ -257,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
     const T* gr = dy + row * cols;
     float dot = 0.f;
     for (int c = threadIdx.x; c < cols; c += kThreads) dot += to_f32(gr[c]) * to_f32(w[c]) * (to_f32(xr[c]) * r);
-    dot = row_sum<kThreads>(dot, red) * inv_cols;
+    dot = row_sum<kThreads, kThreads>(dot, red) * inv_cols;
     T* dxr = dx + row * cols;
     for (int c = threadIdx.x; c < cols; c += kThreads) {
       const float g = to_f32(gr[c]);
@@ -269,25 +302,28 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
   }
 }
 
-// dw[c] = sum over parts of part[p][c], in a fixed order. 64 columns per
-// block, 4 waves splitting the parts, combined through LDS.
-template <typename T>
-__global__ __launch_bounds__(kThreads) void column_sum(const float* __restrict__ part, T* __restrict__ out,
-                                                       int64_t parts, int cols) {
-  __shared__ float acc[kWaves][64];
-  const int c = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int wave = threadIdx.x / 64;
+// Column sums of a [parts, cols] fp32 array in a fixed order. Stage one:
+// block (cx, s) sums parts [s*kColSplit, (s+1)*kColSplit) of 256 columns into
+// stage[s]; stage two sums the stage rows and rounds to T.
+__global__ __launch_bounds__(kThreads) void column_sum_stage(const float* __restrict__ part,
+                                                            float* __restrict__ stage, int64_t parts, int cols) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  const int64_t p0 = (int64_t)blockIdx.y * kColSplit;
+  const int64_t p1 = p0 + kColSplit < parts ? p0 + kColSplit : parts;
+  if (c >= cols) return;
   float s = 0.f;
-  if (c < cols)
-    for (int64_t p = wave; p < parts; p += kWaves) s += part[p * cols + c];
-  acc[wave][threadIdx.x & 63] = s;
-  __syncthreads();
-  if (wave == 0 && c < cols) {
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) t += acc[i][threadIdx.x];
-    out[c] = from_f32<T>(t);
-  }
+  for (int64_t p = p0; p < p1; ++p) s += part[p * cols + c];
+  stage[(int64_t)blockIdx.y * cols + c] = s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void column_sum_final(const float* __restrict__ stage, T* __restrict__ out,
+                                                            int64_t n, int cols) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int64_t p = 0; p < n; ++p) s += stage[p * cols + c];
+  out[c] = from_f32<T>(s);
 }
 
 // ---------------------------------------------------------------------------
@@ -295,124 +331,198 @@ __global__ __launch_bounds__(kThreads) void column_sum(const float* __restrict__
 
 struct Plan {
   bool vec;  // fast path usable
-  int tpr;   // 64 or 256
-  int vpt;   // 1, 2, 4, 8
+  int ntb;   // threads per block
+  int tpr;   // threads per row: 64 or ntb
+  int vpt;   // 16-byte packs per thread: 1, 2, 4, 8, 16
 };
 
-Plan plan_for(int64_t cols, int esize, bool aligned) {
-  const int P = 16 / esize;
-  Plan p{false, kThreads, 1};
-  if (!aligned || cols % P != 0) return p;
-  const int64_t nvec = cols / P;
-  if (nvec > (int64_t)kThreads * kMaxVpt) return p;
-  p.vec = true;
-  p.tpr = nvec <= 64 * kMaxVpt ? 64 : kThreads;
-  int64_t need = (nvec + p.tpr - 1) / p.tpr;
-  p.vpt = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+int pow2_at_least(int64_t n) {
+  int p = 1;
+  while (p < n) p *= 2;
   return p;
 }
 
-int64_t bwd_blocks(int64_t rows, const Plan& p) {
-  const int64_t rpb = p.vec ? kThreads / p.tpr : 1;
-  const int64_t want = (rows + rpb - 1) / rpb;
-  return want < kBwdMaxBlocks ? want : kBwdMaxBlocks;
+// Launch shape for rows of `cols` elements of `esize` bytes: one row per
+// wavefront up to 4 packs per lane, wider rows over a block at 4 packs per
+// thread (forward) or 2 (backward, which also keeps dw columns in
+// registers). Measured on MI355X these beat one-wave rows of 16 packs and
+// blocks of 128 / 512 / 1024 threads for 4096-wide fp32 and 8192-wide bf16
+// rows.
+Plan plan_for(int64_t cols, int esize, bool aligned, bool backward) {
+  const int P = 16 / esize;
+  Plan p{false, kThreads, kThreads, 1};
+  if (!aligned || cols % P != 0) return p;
+  const int64_t nvec = cols / P;
+  const int wave_max = 4;
+  const int block_vpt = backward ? 2 : 4;
+  if (nvec > (int64_t)1024 * kMaxVpt) return p;
+  p.vec = true;
+  if (nvec <= 64 * wave_max) {  // one wave per row, 4 rows per block
+    p.ntb = 256;
+    p.tpr = 64;
+    p.vpt = pow2_at_least((nvec + 63) / 64);
+  } else {  // a block per row
+    p.vpt = block_vpt;
+    p.ntb = p.tpr = pow2_at_least((nvec + p.vpt - 1) / p.vpt);
+    if (p.ntb > 1024) {
+      p.ntb = p.tpr = 1024;
+      p.vpt = pow2_at_least((nvec + 1023) / 1024);
+    }
+  }
+  return p;
 }
 
-int64_t bwd_parts(int64_t rows, const Plan& p) { return bwd_blocks(rows, p) * (p.vec ? kThreads / p.tpr : 1); }
+// Resident blocks per CU of a kernel at this launch shape (queried once per
+// instantiation; each CU of an MI355X is alike).
+template <typename K> int resident_per_cu(K kernel, int threads, size_t lds) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) n = 1;
+  return n;
+}
 
-template <typename T, bool BIAS, int TPR, int VPT>
+template <typename T, bool BIAS, int NTB, int TPR, int VPT> int bwd_resident(int cols) {
+  // dynamic LDS of a 4-rows-per-block shape: one fp32 row of at most 64*4*8 columns
+  static const int n = resident_per_cu(rmsnorm_bwd_vec<T, NTB, TPR, VPT, BIAS>, NTB,
+                                       NTB / TPR > 1 ? (size_t)64 * 4 * 8 * sizeof(float) : 0);
+  (void)cols;
+  return n;
+}
+
+template <typename T, bool BIAS> int bwd_any_resident() {
+  static const int n = resident_per_cu(rmsnorm_bwd_any<T, BIAS>, kThreads, 0);
+  return n;
+}
+
+template <typename T, bool BIAS, int NTB, int TPR, int VPT>
 void launch_fwd_vec(int64_t rows, const void* x, const void* w, const void* b, void* y, float* rstd, int cols,
                     float eps, hipStream_t s) {
-  constexpr int RPB = kThreads / TPR;
-  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, TPR, VPT, BIAS>), dim3((rows + RPB - 1) / RPB), dim3(kThreads), 0, s,
+  constexpr int RPB = NTB / TPR;
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>), dim3((rows + RPB - 1) / RPB), dim3(NTB), 0, s,
                      static_cast<const T*>(x), static_cast<const T*>(w), static_cast<const T*>(b),
                      static_cast<T*>(y), rstd, rows, cols, eps, 1.0f / (float)cols);
-}
-
-template <typename T, bool BIAS, int TPR>
-void dispatch_fwd_vpt(int vpt, int64_t rows, const void* x, const void* w, const void* b, void* y, float* rstd,
-                      int cols, float eps, hipStream_t s) {
-  switch (vpt) {
-    case 1: return launch_fwd_vec<T, BIAS, TPR, 1>(rows, x, w, b, y, rstd, cols, eps, s);
-    case 2: return launch_fwd_vec<T, BIAS, TPR, 2>(rows, x, w, b, y, rstd, cols, eps, s);
-    case 4: return launch_fwd_vec<T, BIAS, TPR, 4>(rows, x, w, b, y, rstd, cols, eps, s);
-    default: return launch_fwd_vec<T, BIAS, TPR, 8>(rows, x, w, b, y, rstd, cols, eps, s);
-  }
-}
-
-template <typename T, bool BIAS>
-int fwd(const void* x, const void* w, const void* b, void* y, float* rstd, int64_t rows, int64_t cols, float eps,
-        hipStream_t s) {
-  const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!BIAS || aligned16(b));
-  const Plan p = plan_for(cols, sizeof(T), aligned);
-  if (!p.vec) {
-    hipLaunchKernelGGL((rmsnorm_fwd_any<T, BIAS>), dim3(rows), dim3(kThreads), 0, s, static_cast<const T*>(x),
-                       static_cast<const T*>(w), static_cast<const T*>(b), static_cast<T*>(y), rstd, rows,
-                       (int)cols, eps, 1.0f / (float)cols);
-  } else if (p.tpr == 64) {
-    dispatch_fwd_vpt<T, BIAS, 64>(p.vpt, rows, x, w, b, y, rstd, (int)cols, eps, s);
-  } else {
-    dispatch_fwd_vpt<T, BIAS, kThreads>(p.vpt, rows, x, w, b, y, rstd, (int)cols, eps, s);
-  }
-  return launched("pk_rmsnorm_fwd");
 }
 
 struct BwdArgs {
   const void *x, *w, *dy;
   const float* rstd;
   void *dx, *dw, *db;
-  float *dw_part, *db_part;
+  float *dw_part, *db_part, *stage;
   int64_t rows;
   int cols;
   hipStream_t s;
 };
 
-template <typename T, bool BIAS, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
+template <typename T, bool BIAS, int NTB, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
+  constexpr int RPB = NTB / TPR;
   const int64_t per = (a.rows + blocks - 1) / blocks;
-  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, TPR, VPT, BIAS>), dim3(blocks), dim3(kThreads), 0, a.s,
+  const size_t lds = RPB > 1 ? (size_t)a.cols * sizeof(float) : 0;
+  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, NTB, TPR, VPT, BIAS>), dim3(blocks), dim3(NTB), lds, a.s,
                      static_cast<const T*>(a.x), static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy),
                      static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols, per);
 }
 
-template <typename T, bool BIAS, int TPR> void dispatch_bwd_vpt(int vpt, const BwdArgs& a, int64_t blocks) {
-  switch (vpt) {
-    case 1: return launch_bwd_vec<T, BIAS, TPR, 1>(a, blocks);
-    case 2: return launch_bwd_vec<T, BIAS, TPR, 2>(a, blocks);
-    case 4: return launch_bwd_vec<T, BIAS, TPR, 4>(a, blocks);
-    default: return launch_bwd_vec<T, BIAS, TPR, 8>(a, blocks);
+// Every (ntb, tpr, vpt) the planner can return.
+#define PK_RMS_FWD_SHAPES(X) X(256, 64, 1) X(256, 64, 2) X(256, 64, 4) X(128, 128, 4) X(256, 256, 4) X(512, 512, 4) \
+  X(1024, 1024, 4) X(1024, 1024, 8) X(1024, 1024, 16)
+#define PK_RMS_BWD_SHAPES(X) X(256, 64, 1) X(256, 64, 2) X(256, 64, 4) X(256, 256, 2) X(512, 512, 2) \
+  X(1024, 1024, 2) X(1024, 1024, 4) X(1024, 1024, 8) X(1024, 1024, 16)
+
+template <typename T, bool BIAS>
+int fwd(const void* x, const void* w, const void* b, void* y, float* rstd, int64_t rows, int64_t cols, float eps,
+        hipStream_t s) {
+  const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!BIAS || aligned16(b));
+  const Plan p = plan_for(cols, sizeof(T), aligned, false);
+  bool done = false;
+#define PK_FWD_CASE(NTB, TPR, VPT)                                                         \
+  if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
+    launch_fwd_vec<T, BIAS, NTB, TPR, VPT>(rows, x, w, b, y, rstd, (int)cols, eps, s);    \
+    done = true;                                                                           \
   }
+  PK_RMS_FWD_SHAPES(PK_FWD_CASE)
+#undef PK_FWD_CASE
+  if (!done)
+    hipLaunchKernelGGL((rmsnorm_fwd_any<T, BIAS>), dim3(rows), dim3(kThreads), 0, s, static_cast<const T*>(x),
+                       static_cast<const T*>(w), static_cast<const T*>(b), static_cast<T*>(y), rstd, rows,
+                       (int)cols, eps, 1.0f / (float)cols);
+  return launched("pk_rmsnorm_fwd");
+}
+
+// Persistent backward grid: every resident block slot of the device, never
+// more blocks than the rows need.
+template <typename T, bool BIAS> int64_t bwd_blocks(int64_t rows, const Plan& p) {
+  int per_cu = 0;
+  int64_t rpb = 1;
+#define PK_RES_CASE(NTB, TPR, VPT)                                                         \
+  if (!per_cu && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                 \
+    per_cu = bwd_resident<T, BIAS, NTB, TPR, VPT>(0);                                     \
+    rpb = NTB / TPR;                                                                       \
+  }
+  PK_RMS_BWD_SHAPES(PK_RES_CASE)
+#undef PK_RES_CASE
+  if (!per_cu) per_cu = bwd_any_resident<T, BIAS>();
+  const int64_t want = (rows + rpb - 1) / rpb;
+  const int64_t cap = (int64_t)cu_count() * per_cu;
+  return want < cap ? want : cap;
+}
+
+int64_t stage_rows(int64_t parts) { return (parts + kColSplit - 1) / kColSplit; }
+
+template <typename T> void column_sums(const float* part, float* stage, T* out, int64_t parts, int cols,
+                                       hipStream_t s) {
+  const int64_t n = stage_rows(parts);
+  const int cx = (cols + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(column_sum_stage, dim3(cx, (unsigned)n), dim3(kThreads), 0, s, part, stage, parts, cols);
+  hipLaunchKernelGGL(column_sum_final<T>, dim3(cx), dim3(kThreads), 0, s, stage, out, n, cols);
 }
 
 template <typename T, bool BIAS> int bwd(const BwdArgs& a) {
   const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.dy) && aligned16(a.dx);
-  const Plan p = plan_for(a.cols, sizeof(T), aligned);
-  const int64_t blocks = bwd_blocks(a.rows, p);
-  if (!p.vec) {
+  const Plan p = plan_for(a.cols, sizeof(T), aligned, true);
+  const int64_t blocks = bwd_blocks<T, BIAS>(a.rows, p);
+  bool done = false;
+#define PK_BWD_CASE(NTB, TPR, VPT)                                                         \
+  if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
+    launch_bwd_vec<T, BIAS, NTB, TPR, VPT>(a, blocks);                                    \
+    done = true;                                                                           \
+  }
+  PK_RMS_BWD_SHAPES(PK_BWD_CASE)
+#undef PK_BWD_CASE
+  if (!done) {
     const int64_t per = (a.rows + blocks - 1) / blocks;
     hipLaunchKernelGGL((rmsnorm_bwd_any<T, BIAS>), dim3(blocks), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
                        static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy), static_cast<T*>(a.dx),
                        a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols, per);
-  } else if (p.tpr == 64) {
-    dispatch_bwd_vpt<T, BIAS, 64>(p.vpt, a, blocks);
-  } else {
-    dispatch_bwd_vpt<T, BIAS, kThreads>(p.vpt, a, blocks);
   }
-  const int64_t parts = bwd_parts(a.rows, p);
-  const dim3 grid((a.cols + 63) / 64);
-  hipLaunchKernelGGL(column_sum<T>, grid, dim3(kThreads), 0, a.s, a.dw_part, static_cast<T*>(a.dw), parts, a.cols);
-  if (BIAS)
-    hipLaunchKernelGGL(column_sum<T>, grid, dim3(kThreads), 0, a.s, a.db_part, static_cast<T*>(a.db), parts, a.cols);
+  column_sums<T>(a.dw_part, a.stage, static_cast<T*>(a.dw), blocks, a.cols, a.s);
+  if (BIAS) column_sums<T>(a.db_part, a.stage, static_cast<T*>(a.db), blocks, a.cols, a.s);
   return launched("pk_rmsnorm_bwd");
 }
 
-int64_t workspace_bytes(int64_t rows, int64_t cols, int dtype, bool bias) {
-  // Plan with alignment assumed: the vec plan needs at least as many parts
-  // as the fallback, so the size covers both.
-  const Plan p = plan_for(cols, elem_size(dtype), true);
-  const int64_t parts = bwd_parts(rows, p);
-  int64_t one = parts * cols * (int64_t)sizeof(float);
-  one = (one + 255) / 256 * 256;
-  return bias ? 2 * one : one;
+// Workspace: [blocks, cols] dw partials, the same for dbias, and the
+// [stage_rows, cols] first-stage column sums, each rounded up to 256 bytes.
+struct Layout {
+  int64_t part, stage, total;
+};
+
+template <typename T, bool BIAS> Layout layout_for(int64_t rows, int64_t cols) {
+  // The aligned plan and the fallback may use different grids: size for the larger.
+  const int64_t b1 = bwd_blocks<T, BIAS>(rows, plan_for(cols, sizeof(T), true, true));
+  const int64_t b2 = bwd_blocks<T, BIAS>(rows, plan_for(cols, sizeof(T), false, true));
+  const int64_t blocks = b1 > b2 ? b1 : b2;
+  auto up = [](int64_t n) { return (n + 255) / 256 * 256; };
+  Layout l;
+  l.part = up(blocks * cols * (int64_t)sizeof(float));
+  l.stage = up(stage_rows(blocks) * cols * (int64_t)sizeof(float));
+  l.total = l.part * (BIAS ? 2 : 1) + l.stage;
+  return l;
+}
+
+Layout workspace_layout(int64_t rows, int64_t cols, int dtype, bool bias) {
+  switch (dtype) {
+    case PK_F32: return bias ? layout_for<float, true>(rows, cols) : layout_for<float, false>(rows, cols);
+    case PK_BF16: return bias ? layout_for<bf16, true>(rows, cols) : layout_for<bf16, false>(rows, cols);
+    default: return bias ? layout_for<f16, true>(rows, cols) : layout_for<f16, false>(rows, cols);
+  }
 }
 
 int check_shape(const char* who, int64_t rows, int64_t cols, int dtype) {
@@ -450,7 +560,7 @@ int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, floa
 int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype) {
   using namespace pk;
   if (rows <= 0 || cols <= 0 || !known_dtype(dtype)) return 0;
-  return workspace_bytes(rows, cols, dtype, true);
+  return workspace_layout(rows, cols, dtype, true).total;
 }
 
 int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
@@ -462,12 +572,12 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
     return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: null pointer");
   const bool b = dbias != nullptr;
   if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "pk_rmsnorm_bwd: zero rows (dw is all zeros; fill it host-side)");
-  const int64_t need = pk::workspace_bytes(rows, cols, dtype, b);
-  if (workspace_bytes < need)
+  const Layout l = workspace_layout(rows, cols, dtype, b);
+  if (workspace_bytes < l.total)
     return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
-                (long long)need);
+                (long long)l.total);
   if (!aligned16(workspace)) return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: workspace not 16-byte aligned");
-  const int64_t half = need / (b ? 2 : 1);
+  char* base = static_cast<char*>(workspace);
   BwdArgs a{x,
             w,
             dy,
@@ -475,8 +585,9 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
             dx,
             dw,
             dbias,
-            static_cast<float*>(workspace),
-            b ? reinterpret_cast<float*>(static_cast<char*>(workspace) + half) : nullptr,
+            reinterpret_cast<float*>(base),
+            b ? reinterpret_cast<float*>(base + l.part) : nullptr,
+            reinterpret_cast<float*>(base + l.part * (b ? 2 : 1)),
             rows,
             (int)cols,
             static_cast<hipStream_t>(stream)};

@@ -53,7 +53,8 @@ def _run(shape, dtype, eps, with_bias, seed):
         gauge_ok(grads_m[2], db64, grads_r[2], dtype, "db")
 
 
-SHAPES = [(1, 64), (4, 4096), (3, 1000), (17, 8192), (2, 3, 512), (5, 16384), (2, 20000), (300, 128), (1, 7)]
+SHAPES = [(1, 64), (4, 4096), (3, 1000), (17, 8192), (2, 3, 512), (5, 16384), (2, 20000), (300, 128), (1, 7),
+          (3, 3000), (2, 40000), (1030, 2048)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
