@@ -2,9 +2,8 @@
 // gfx950 matrix cores.
 //
 // Block = 4 wavefronts x 32 query rows (BM = 128) of one (batch, q head);
-// keys stream through LDS in tiles of BN = 64, double-buffered: K and V of
-// tile t+1 are fetched into registers (buffer loads) while tile t is
-// multiplied, then stored to the idle LDS buffer.
+// two blocks share a CU (two waves per SIMD). Keys stream through LDS in
+// tiles of BN = 32.
 //
 // Per tile each wave computes
 //   S^T (32 keys x 32 queries)  = K_tile . Q^T   (v_mfma_f32_32x32x16, K from
@@ -12,38 +11,50 @@
 //   O^T (head_dim x 32 queries) += V^T . P^T
 // Working on transposes puts one query per lane column: the MFMA result
 // layout gives lane l the 16 entries of query l%32 in key rows
-// 8*(r/4) + 4*(l/32) + r%4, so the online-softmax row max / sum are in-lane
-// except for one exchange with lane l^32, and the rescale of O^T by that
-// query's alpha is lane-uniform. P leaves the accumulator registers directly
-// as the B operand of the second product: the key order inside each
-// 16-key MFMA step is permuted identically in P^T and in the V^T fragments,
-// which the contraction does not see.
+// 8*(r/4) + 4*(l/32) + r%4, so the softmax sums are in-lane except for one
+// exchange with lane l^32. P leaves the accumulator registers directly as the
+// B operand of the second product: the key order inside each 16-key MFMA
+// step is permuted identically in P^T and in the V^T fragments, which the
+// contraction does not see.
+//
+// Software pipeline (per wave): step t masks S(t), exponentiates it and
+// multiplies P(t) into O while the matrix cores compute S(t+1) from the
+// next K tile, so the softmax arithmetic of one tile overlaps the matrix
+// work of the next. Staging runs ahead of that: the step issues the global
+// loads of K(t+2) and V(t+1) and stores them to LDS at its end, into
+// buffers every wave has finished with; one barrier per step.
+//
+// Softmax with a fixed reference max: m is the row max of s * c over the
+// first key tile (key 0 is visible to every row) and stays put, so no step
+// computes a row max or rescales O; p = exp2(s * c - m) is one FMA plus one
+// exp, with c = |scale| * log2(e) (a negative scale negates Q on load, which
+// is exact). Later scores may exceed m: o = acc / l and lse = m + log(l) are
+// unchanged by the choice of m as long as P and the sums stay in range, which
+// holds while l stays below 2^32 (2^15 for fp16, whose P must fit in fp16:
+// every p is at most l). A block where some row's l leaves that range, or is
+// not finite, sweeps its keys again with the exact online max (rescaling O
+// when the max grows by more than 2^8), so the result never depends on the
+// data being benign. The log-sum-exp output is converted back to natural log.
 //
 // LDS layouts:
-//   K [BN][D]: 16-byte chunk c of row r sits at chunk position c ^ (r % (D/8)),
-//       so the 16-byte fragment reads of consecutive rows hit distinct banks.
-//   V [BN][D + 16]: row-major. V^T fragments come from ds_read_b64_tr_b16:
-//       within a 16-lane group, lane s reads keys base + s/4, dims
-//       d0 + 4*(s%4) .. +3, and lane i receives dims d0 + i of keys
-//       base .. base + 3 -- half of one MFMA A fragment; the padding puts the
-//       four rows of one read on different banks.
+//   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272
+//       (or 144) bytes apart and so cover all 64 banks once.
+//   V [BN][D + 32]: row-major, rows 64 bytes apart modulo 256. V^T fragments
+//       come from ds_read_b64_tr_b16: within a 16-lane group, lane s reads
+//       keys base + s/4, dims d0 + 4*(s%4) .. +3, and lane i receives dims
+//       d0 + i of keys base .. base + 3 -- half of one MFMA A fragment. The
+//       two 16-lane groups served together read 4 rows x 64 bytes, which the
+//       row offset spreads over all 64 banks.
 //
 // K and V are read through buffer resources based at the (batch, kv head):
 // a tile is one scalar offset, and rows at or past S read as zero, so no load
-// is predicated; such keys are masked like causal ones.
-//
-// Softmax runs in base 2: raw scores s are reduced to a row max first and
-// exp2(s * c - m) is one FMA plus one exp with c = |scale| * log2(e) (a
-// negative scale negates Q on load, which is exact). The running max m only
-// moves when some query's candidate exceeds it by more than 8: exponents stay
-// <= 8, and o = acc / l uses the same m in both, so the result is unchanged
-// while most tiles skip the O rescale. The log-sum-exp output is converted
-// back to natural log. Causal blocks only visit key tiles up to their last
-// query and a wave skips the MFMAs of a tile wholly above its diagonal. Work
-// order: longest causal rows first, and the q heads sharing a kv head land on
-// the same XCD (dispatch is round-robin over the 8 XCDs), so their K/V tiles
-// are shared through that XCD's L2.
+// is predicated; such keys are masked like causal ones. Work order: longest
+// causal rows first, and the q heads sharing a kv head land on the same XCD
+// (dispatch is round-robin over the 8 XCDs), so their K/V tiles are shared
+// through that XCD's L2.
 #include <math.h>
+
+#include <type_traits>
 
 #include "api.h"
 #include "common.h"
@@ -54,9 +65,11 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s4;
 
 constexpr int BM = 128;
-constexpr int BN = 64;
+constexpr int BN = 32;
 constexpr int NT = 256;
 
 template <typename T> struct Mma;
@@ -73,6 +86,10 @@ template <> struct Mma<f16> {
   }
 };
 
+// Largest row sum the fixed-max sweep accepts (see the header).
+template <typename T> constexpr float kFastLimit = 4294967296.0f;
+template <> constexpr float kFastLimit<f16> = 32768.0f;
+
 struct AttnArgs {
   const void* q;
   const void* k;
@@ -82,13 +99,9 @@ struct AttnArgs {
   int64_t qsb, qss, qsh, ksb, kss, ksh, vsb, vss, vsh, osb, oss, osh;
   int B, S, Hq, Hkv, group, m_tiles;
   int k_bytes, v_bytes;  // bytes from a (batch, kv head) base to the end of its last row
-  float c;          // |scale| * log2(e), at least 1e-30
-  uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
+  float c;               // |scale| * log2(e), at least 1e-30
+  uint32_t q_flip;       // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) s16x4 lds_s4;
 
 __device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
   typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
@@ -100,12 +113,14 @@ template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_fwd_kernel(
     AttnArgs a) {
   using Frag = typename Mma<T>::frag;
-  constexpr int KST = D;       // K row stride in LDS, elements (16-byte chunks XOR-swizzled by row)
-  constexpr int VST = D + 16;  // V row stride in LDS, elements (row-major; read transposed)
+  constexpr int KST = D + 8;   // K row stride in LDS, elements
+  constexpr int VST = D + 32;  // V row stride in LDS, elements
   constexpr int KCH = D / 8;   // 16-byte chunks per K/V row
   constexpr int K_ROWS = NT / KCH;
-  constexpr int K_PASSES = BN / K_ROWS;
-  constexpr int V_RPT = BN * KCH / NT;  // consecutive V rows per thread
+  constexpr int K_PASSES = BN / K_ROWS;  // K rows per thread, K_ROWS apart
+  constexpr int V_RPT = BN * KCH / NT;   // consecutive V rows per thread
+  constexpr int KK = D / 16;
+  constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
   __shared__ __attribute__((aligned(16))) T Vs[2][BN * VST];
 
@@ -129,12 +144,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int hq = hkv * G + hig;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r32 = lane & 31;
   const int g = lane >> 5;
   const int m0 = m_tile * BM;
-  const int q_row = m0 + wave * 32 + r32;
+  const int wave_first = m0 + wave * 32;
+  const int q_row = wave_first + r32;
 
   const T* qbase = static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh;
   const T* kbase = static_cast<const T*>(a.k) + b * a.ksb + hkv * a.ksh;
@@ -147,156 +163,193 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
       __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, a.v_bytes, 0x00020000);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
-  Frag qf[D / 16];
+  Frag qf[KK];
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
+  for (int kk = 0; kk < KK; ++kk) {
     uint4 raw = make_uint4(0, 0, 0, 0);
     if (q_row < a.S) raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
     raw.x ^= a.q_flip;
     raw.y ^= a.q_flip;
     raw.z ^= a.q_flip;
     raw.w ^= a.q_flip;
-    qf[kk] = *reinterpret_cast<const Frag*>(&raw);
+    qf[kk] = __builtin_bit_cast(Frag, raw);
   }
 
-  const int kv_end = CAUSAL ? (m0 + BM < a.S ? m0 + BM : a.S) : a.S;
+  const int kv_end = CAUSAL ? min(m0 + BM, a.S) : a.S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
   // ---- tile staging: K rows by 16-byte chunk, V rows V_RPT at a time
   const int kc = tid % KCH, kr = tid / KCH;
-  const int vr = (tid / KCH) * V_RPT;
+  const int vr = kr * V_RPT;
   const int koff = (kr * (int)a.kss + kc * 8) * (int)sizeof(T);  // byte offset of this lane's first K chunk
   const int voff = (vr * (int)a.vss + kc * 8) * (int)sizeof(T);
   uint4 kreg[K_PASSES], vreg[V_RPT];
-  // this lane's element offsets of its K fragments (row r32, chunk 2kk + g, swizzled)
-  int k_lane[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) k_lane[kk] = r32 * KST + (((2 * kk + g) ^ (r32 & (KCH - 1))) * 8);
-  // this lane's element offset for the transposing V reads (see the PV loop)
+  // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
+  // dims 16kk + 8g ..), and the transposing V reads (see pv)
+  const int k_lane = r32 * KST + 8 * g;
   const int v_lane = (4 * g + ((lane & 15) >> 2)) * VST + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  f32x16 acc[D / 32];
+  auto load_k = [&](int t) {
+    const int tile = t * BN * (int)a.kss * (int)sizeof(T);
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+    for (int p = 0; p < K_PASSES; ++p) kreg[p] = ld_buf(krsrc, koff + p * K_ROWS * (int)a.kss * (int)sizeof(T), tile);
+  };
+  auto load_v = [&](int t) {
+    const int tile = t * BN * (int)a.vss * (int)sizeof(T);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
-  float m_i = -INFINITY;  // running max of s * c for query q_row
-  float l_i = 0.f;        // this lane's half of the running denominator
+    for (int i = 0; i < V_RPT; ++i) vreg[i] = ld_buf(vrsrc, voff + i * (int)a.vss * (int)sizeof(T), tile);
+  };
+  auto store_k = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < K_PASSES; ++p) *reinterpret_cast<uint4*>(Ks[buf] + (kr + p * K_ROWS) * KST + kc * 8) = kreg[p];
+  };
+  auto store_v = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < V_RPT; ++i) *reinterpret_cast<uint4*>(Vs[buf] + (vr + i) * VST + kc * 8) = vreg[i];
+  };
+  // S^T of the K tile in buffer buf
+  auto scores = [&](int buf) {
+    const T* ks = Ks[buf];
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s = Mma<T>::run(*reinterpret_cast<const Frag*>(ks + k_lane + 16 * kk), qf[kk], s);
+    return s;
+  };
+  // whether tile t holds keys some row of this wave must not see
+  auto need_mask = [&](int t) { return (CAUSAL && t * BN + BN - 1 > wave_first) || t * BN + BN > a.S; };
+  auto apply_mask = [&](int t, f32x16& s) {
+    // last visible key of this lane's query; rows past the end (zero loads) are masked too
+    const int lim = CAUSAL ? min(q_row, a.S - 1) : a.S - 1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = t * BN + 8 * (r >> 2) + 4 * g + (r & 3);
+      s[r] = key <= lim ? s[r] : -INFINITY;
+    }
+  };
+  f32x16 acc[DT];
+  // O^T += V^T P^T over the tile's two 16-key steps. V^T fragments come from
+  // transposing reads of row-major V: within each 16-lane group, lane s reads
+  // keys (base + s/4), dims (d0 + 4*(s%4)) .. +3, and lane i receives dims
+  // d0 + i of keys base .. base + 3.
+  auto pv = [&](int buf, const Frag (&pf)[2]) {
+    lds_s4* vt = (lds_s4*)(Vs[buf] + v_lane);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
+        acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf[c],
+                              acc[dt]);
+      }
+  };
+  float m_i;  // reference max of s * c for query q_row
+  float l_i;  // this lane's half of the denominator
+  // P = exp2(s * c - m) as the B fragments of the two 16-key steps; l += row sum
+  auto softmax = [&](const f32x16& s, float m_use, Frag (&pf)[2]) {
+    float rs = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c + j], a.c, -m_use));
+        rs += p;
+        pf[c][j] = (T)p;
+      }
+    l_i += rs;
+  };
+  auto clear = [&]() {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+    l_i = 0.f;
+  };
 
-#define PK_LOAD_TILE(t)                                                                                        \
-  do {                                                                                                         \
-    const int ktile_ = (t)*BN * (int)a.kss * (int)sizeof(T);                                                   \
-    const int vtile_ = (t)*BN * (int)a.vss * (int)sizeof(T);                                                   \
-    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p)                                                       \
-      kreg[p] = ld_buf(krsrc, koff + p * K_ROWS * (int)a.kss * (int)sizeof(T), ktile_);                       \
-    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i)                                                          \
-      vreg[i] = ld_buf(vrsrc, voff + i * (int)a.vss * (int)sizeof(T), vtile_);                                \
-  } while (0)
-
-#define PK_STORE_TILE(buf)                                                                                     \
-  do {                                                                                                         \
-    T* ks_ = Ks[buf];                                                                                          \
-    _Pragma("unroll") for (int p = 0; p < K_PASSES; ++p)                                                       \
-        *reinterpret_cast<uint4*>(ks_ + (kr + p * K_ROWS) * KST + (kc ^ ((kr + p * K_ROWS) & (KCH - 1))) * 8) = kreg[p]; \
-    T* vs_ = Vs[buf];                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < V_RPT; ++i)                                                          \
-        *reinterpret_cast<uint4*>(vs_ + (vr + i) * VST + kc * 8) = vreg[i];                                   \
-  } while (0)
-
-  PK_LOAD_TILE(0);
-  PK_STORE_TILE(0);
+  // ---- fast sweep: fixed max, S(t+1) pipelined with the softmax and PV of tile t
+  clear();
+  load_k(0);
+  load_v(0);
+  store_k(0);
+  store_v(0);
+  load_k(1);  // past the end this reads zeros or keys nobody uses
+  store_k(1);
   __syncthreads();
+  f32x16 sa = scores(0), sb;
+  if (need_mask(0)) apply_mask(0, sa);
+  {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[r]);
+    m_i = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.c;
+  }
+  __syncthreads();  // K(0) is read; the first step overwrites its buffer
+  Frag pf[2];
+  // Step t: S(t) in cur, S(t+1) into nxt. Buffers: K(t+1) in Ks[(t+1)&1] and
+  // V(t) in Vs[t&1] are read; K(t+2) goes to Ks[t&1] and V(t+1) to
+  // Vs[(t+1)&1], whose previous tiles were last read in step t-1.
+  auto step = [&](int t, f32x16& cur, f32x16& nxt) {
+    if (need_mask(t)) apply_mask(t, cur);
+    load_k(t + 2);
+    load_v(min(t + 1, n_tiles - 1));
+    nxt = scores((t + 1) & 1);
+    softmax(cur, m_i, pf);
+    pv(t & 1, pf);
+    store_k(t & 1);
+    store_v((t + 1) & 1);
+    __syncthreads();
+  };
+  // pairs of steps keep each S in fixed registers; one exit keeps O in place
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    step(t, sa, sb);
+    step(t + 1, sb, sa);
+  }
+  if (t < n_tiles) step(t, sa, sb);
 
-  const int wave_first = m0 + wave * 32;
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    // The last iteration re-reads its own tile into the idle buffer: the
-    // staging registers never sit behind a branch, which keeps them in VGPRs.
-    PK_LOAD_TILE(min(t + 1, n_tiles - 1));
-    const int kv0 = t * BN;
-    if (!(CAUSAL && kv0 > wave_first + 31)) {
-      const T* ks = Ks[buf];
-      f32x16 s[2];
+  {
+    const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+    const bool bad = !(l_tot <= kFastLimit<T>) || !(fabsf(m_i) < INFINITY);
+    if (__syncthreads_or(bad)) {
+      // ---- exact sweep: online max; O and l are rescaled only when the max
+      // grows by more than 2^8 (exponents stay <= 8, and o = acc / l uses the
+      // same max in both)
+      clear();
+      m_i = -INFINITY;
+      load_k(0);
+      load_v(0);
+      store_k(0);
+      store_v(0);
+      __syncthreads();
+      for (int u = 0; u < n_tiles; ++u) {
+        load_k(min(u + 1, n_tiles - 1));
+        load_v(min(u + 1, n_tiles - 1));
+        f32x16 s = scores(u & 1);
+        if (need_mask(u)) apply_mask(u, s);
+        float mx = -INFINITY;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+        const float m_cand = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.c;
+        if (!__all(m_cand <= m_i + 8.0f)) {
+          const float m_new = fmaxf(m_i, m_cand);
+          const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);  // 0 when m_i = -inf
+          l_i *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[st][r] = 0.f;
+          for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const Frag kf = *reinterpret_cast<const Frag*>(ks + st * 32 * KST + k_lane[kk]);
-          s[st] = Mma<T>::run(kf, qf[kk], s[st]);
+            for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+          m_i = m_new;
         }
-      }
-      // mask, row max of the raw scores
-      const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > a.S;
-      if (need_mask) {
-        // last visible key of this lane's query; rows past the end (clamped loads) are masked too
-        const int lim = CAUSAL ? min(q_row, a.S - 1) : a.S - 1;
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + st * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            s[st][r] = key <= lim ? s[st][r] : -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[st][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // The running max only moves when some query's max grew by more than
-      // 2^8: exponents then stay <= 8 (p <= 256, exact in bf16 range) and the
-      // final o = acc / l uses the same stale max in both, so the result is
-      // unchanged while most tiles skip the O rescale entirely.
-      const float m_cand = mx * a.c;
-      if (!__all(m_cand <= m_i + 8.0f)) {
-        const float m_new = fmaxf(m_i, m_cand);
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);  // 0 when m_i = -inf
-        l_i *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-        m_i = m_new;
-      }
-      const float m_use = m_i == -INFINITY ? 0.f : m_i;
-      float rs = 0.f;
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[st][r], a.c, -m_use));
-          s[st][r] = p;
-          rs += p;
-        }
-      l_i += rs;
-
-      // O^T += V^T P^T, four 16-key steps
-      // V^T fragments by transposing reads of row-major V: within each 16-lane
-      // group, lane s reads keys (base + s/4), dims (d0 + 4*(s%4)) .. +3, and
-      // lane i receives dims d0 + i of keys base .. base + 3.
-      lds_s4* vt = (lds_s4*)(Vs[buf] + v_lane);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        Frag pf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pf[j] = (T)s[c >> 1][8 * (c & 1) + j];
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
-          const s16x8 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, both), pf, acc[dt]);
-        }
+        softmax(s, m_i == -INFINITY ? 0.f : m_i, pf);
+        pv(u & 1, pf);
+        store_k((u + 1) & 1);
+        store_v((u + 1) & 1);
+        __syncthreads();
       }
     }
-    PK_STORE_TILE(buf ^ 1);
-    __syncthreads();
   }
-#undef PK_LOAD_TILE
-#undef PK_STORE_TILE
 
   // ---- epilogue
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
@@ -304,7 +357,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   if (q_row < a.S) {
     T* orow = static_cast<T*>(a.o) + b * a.osb + hq * a.osh + (int64_t)q_row * a.oss;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d0 = dt * 32 + 8 * rq + 4 * g;
@@ -382,9 +435,11 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   a.Hkv = (int)kv_heads;
   a.group = (int)(q_heads / kv_heads);
   a.m_tiles = (int)((seq + BM - 1) / BM);
-  // buffer offsets are 32-bit: every row offset inside one (batch, kv head) must fit
+  // Buffer offsets are 32-bit: the tile loads reach up to two tiles past the
+  // last one (reading zeros there), and every such offset must fit.
   const int64_t k_span = ((seq - 1) * strides[4] + head_dim) * 2, v_span = ((seq - 1) * strides[7] + head_dim) * 2;
-  if (k_span > INT32_MAX - 4096 || v_span > INT32_MAX - 4096)
+  const int64_t reach = (seq + 3 * BN) * (strides[4] > strides[7] ? strides[4] : strides[7]) * 2 + head_dim * 2;
+  if (reach > INT32_MAX)
     return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: K/V rows span more than 2 GiB per head");
   a.k_bytes = (int)k_span;
   a.v_bytes = (int)v_span;

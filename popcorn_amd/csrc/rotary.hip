@@ -48,13 +48,14 @@ template <int N> __device__ __forceinline__ void load_table(const float* p, floa
   }
 }
 
-// Loads/stores VEC consecutive elements of T: one 16-byte access when VEC
-// fills it, element accesses otherwise.
+// Loads/stores VEC consecutive elements of T: one 16-byte non-temporal access
+// when VEC fills it (x and y are touched once; the cos/sin rows, reused by
+// every head of a position, stay cacheable), element accesses otherwise.
 template <typename T, int VEC> struct Chunk {
   T v[VEC];
   __device__ __forceinline__ void load(const T* p) {
     if constexpr (VEC * sizeof(T) == 16) {
-      *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(p);
+      *reinterpret_cast<u32x4*>(v) = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[j] = p[j];
@@ -62,7 +63,7 @@ template <typename T, int VEC> struct Chunk {
   }
   __device__ __forceinline__ void store(T* p) const {
     if constexpr (VEC * sizeof(T) == 16) {
-      *reinterpret_cast<uint4*>(p) = *reinterpret_cast<const uint4*>(v);
+      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(v), reinterpret_cast<u32x4*>(p));
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) p[j] = v[j];

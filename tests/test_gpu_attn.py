@@ -109,3 +109,40 @@ def test_attn_c5_full_size():
         )[0]
         gauge_ok(o[b, rows, h], o64, ref, torch.bfloat16, f"o[{b},:,{h}]")
         np.testing.assert_allclose(lse[b, h, rows].cpu().double().numpy(), lse64, rtol=0, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("seq", [100, 777])
+def test_attn_late_large_scores(seq, causal, dtype):
+    """Scores far above the first key tile's max (boosted keys at 60..69 and
+    boosted queries from row 80 on): the fixed-max sweep's row sums leave its
+    range, and those blocks must sweep again with the online max."""
+    b, hq, hkv, d = 2, 8, 2, 128
+    q = seeded((b, seq, hq, d), 21, torch.float32)
+    k = seeded((b, seq, hkv, d), 22, torch.float32)
+    v = seeded((b, seq, hkv, d), 23, torch.float32)
+    k[:, 60:70] *= 6.0
+    q[:, 80:] *= 3.0
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    o64, lse64 = O.attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), causal, None)
+    with torch.no_grad():
+        oref = R.attn(q, k, v, causal, None)
+        om, lse = impls.attn_with_lse(q.to(DEV), k.to(DEV), v.to(DEV), causal, None)
+    assert torch.isfinite(om.float()).all()
+    gauge_ok(om, o64, oref, dtype, "o")
+    np.testing.assert_allclose(lse.cpu().double().numpy(), lse64, rtol=0, atol=1e-3)
+
+
+def test_attn_fp16_long_uniform_rows():
+    """fp16, q = 0 over 40000 keys: every row sum is 40000 > 2^15, so the
+    fixed-max sweep hands every block to the exact sweep; o = mean(v), lse = log(S)."""
+    b, s, hq, hkv, d = 1, 40000, 2, 1, 64
+    q = torch.zeros(b, s, hq, d, dtype=torch.float16, device=DEV)
+    k = seeded((b, s, hkv, d), 31, torch.float16).to(DEV)
+    v = seeded((b, s, hkv, d), 32, torch.float16).to(DEV)
+    with torch.no_grad():
+        o, lse = impls.attn_with_lse(q, k, v, False)
+    mean = v.double().mean(dim=1, keepdim=True).expand(b, s, hkv, d).repeat_interleave(hq // hkv, dim=2)
+    assert (o.double() - mean).abs().max().item() < 2e-3
+    assert (lse.double() - np.log(s)).abs().max().item() < 1e-4
