@@ -96,7 +96,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             return nbytes / t / 1e12, f"full C1 x [{rows}, {cols}] fp32, median of {reps} reps"
 
         return Workload("c1", "RMSNorm forward fp32 x [4096, 4096]", "f32", "TB/s", nbytes, step,
-                        "rmsnorm_fwd_vec", nbytes, launch,
+                        "rmsnorm_fwd_grid", nbytes, launch,
                         {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "fp32"}, cpu)
 
     if name == "c2":

@@ -8,13 +8,19 @@
 // whole block (a wave reduction plus one LDS exchange). Any other shape takes
 // a one-block-per-row kernel that loops over the row twice.
 //
-// Backward is a persistent grid (a few blocks per CU): each block walks a
-// contiguous run of rows with w and its running dw / dbias columns in
-// registers, prefetching the next row's x and dy while the current row's dot
-// product is reduced. Blocks leave one fp32 partial row each (the rows of a
-// block's wavefront slots are combined through LDS first), and a two-stage
-// column reduction sums the partials in a fixed order, so dw is
-// deterministic.
+// Forward launches one block per row group, except for row counts that fit in
+// a few waves of resident blocks: there a persistent grid takes rows in grid
+// stride with w in registers and the next row prefetched (measured faster on
+// MI355X for such short launches, slower for long ones).
+//
+// Backward is a persistent grid (a few blocks per CU): block b takes rows
+// b, b + G, b + 2G, ... (G = grid size; the blocks together sweep the tensors
+// front to back, which measured 13% faster than contiguous runs of rows per
+// block) with w and its running dw / dbias columns in registers, prefetching
+// the next row's x and dy while the current row's dot product is reduced.
+// Blocks leave one fp32 partial row each (the rows of a block's wavefront
+// slots are combined through LDS first), and a two-stage column reduction
+// sums the partials in a fixed order, so dw is deterministic.
 #include "api.h"
 #include "common.h"
 
@@ -52,8 +58,7 @@ template <typename T, bool BIAS> __device__ __forceinline__ T fwd_elem(float xv,
   return from_f32<T>(y);
 }
 
-// One row per TPR lanes, RPB = NTB / TPR rows per block. (A persistent
-// variant keeping w in registers measured slower on MI355X.)
+// One row per TPR lanes, RPB = NTB / TPR rows per block.
 template <typename T, int NTB, int TPR, int VPT, bool BIAS>
 __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, const T* __restrict__ w,
                                                        const T* __restrict__ bias, T* __restrict__ y,
@@ -101,6 +106,76 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
         out.v[j] = fwd_elem<T, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv.v[j]), BIAS ? to_f32(bv.v[j]) : 0.f);
       st16_stream(yr + v * P, out);
     }
+  }
+}
+
+// Persistent form of rmsnorm_fwd_vec for short launches: slot s of block b
+// takes rows b * RPB + s + k * stride, with w (and bias) in registers and the
+// next row's x in flight while the current row is reduced.
+template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+__global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x, const T* __restrict__ w,
+                                                        const T* __restrict__ bias, T* __restrict__ y,
+                                                        float* __restrict__ rstd, int64_t rows, int cols, float eps,
+                                                        float inv_cols) {
+  constexpr int P = Vec<T>::N;
+  constexpr int RPB = NTB / TPR;
+  __shared__ float red[NTB / 64];
+  const int lane = threadIdx.x % TPR;
+  const int nvec = cols / P;
+  const int64_t stride = (int64_t)gridDim.x * RPB;
+  const int64_t first = (int64_t)blockIdx.x * RPB;
+  const int64_t row0 = first + threadIdx.x / TPR;
+  const int64_t trips = (rows - first + stride - 1) / stride;  // the same for every slot: barriers line up
+  Vec<T> wv[VPT], bv[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int v = lane + k * TPR;
+    if (v < nvec) {
+      wv[k] = ld16(w + v * P);
+      if constexpr (BIAS) bv[k] = ld16(bias + v * P);
+    }
+  }
+  Vec<T> xv[VPT], xn[VPT];
+  auto fetch = [&](int64_t row, Vec<T>* xo) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int v = lane + k * TPR;
+      if (row < rows && v < nvec) xo[k] = ld16_stream(x + row * cols + v * P);
+    }
+  };
+  fetch(row0, xv);
+  for (int64_t t = 0; t < trips; ++t) {
+    const int64_t row = row0 + t * stride;
+    fetch(row + stride, xn);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int v = lane + k * TPR;
+      if (row < rows && v < nvec)
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+          const float f = to_f32(xv[k].v[j]);
+          ss += f * f;
+        }
+    }
+    ss = row_sum<NTB, TPR>(ss, red);
+    if (row < rows) {
+      const float r = 1.0f / sqrtf(ss * inv_cols + eps);
+      if (rstd != nullptr && lane == 0) rstd[row] = r;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int v = lane + k * TPR;
+        if (v < nvec) {
+          Vec<T> out;
+#pragma unroll
+          for (int j = 0; j < P; ++j)
+            out.v[j] = fwd_elem<T, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv[k].v[j]), BIAS ? to_f32(bv[k].v[j]) : 0.f);
+          st16_stream(y + row * cols + v * P, out);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) xv[k] = xn[k];
   }
 }
 
@@ -177,7 +252,7 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
                                                        const float* __restrict__ rstd, const T* __restrict__ dy,
                                                        T* __restrict__ dx, float* __restrict__ dw_part,
                                                        float* __restrict__ db_part, int64_t rows, int cols,
-                                                       float inv_cols, int64_t rows_per_block) {
+                                                       float inv_cols) {
   constexpr int P = Vec<T>::N;
   constexpr int RPB = NTB / TPR;
   __shared__ float red[NTB / 64];
@@ -200,18 +275,18 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
     }
   }
 
-  // This block owns rows [row0, row_end); slot s takes row0 + s, + RPB, ...
-  const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
-  const int64_t row_end = row0 + rows_per_block < rows ? row0 + rows_per_block : rows;
-  // Every slot runs the same trip count so block-wide barriers line up.
-  const int64_t trips = row_end > row0 ? (row_end - row0 + RPB - 1) / RPB : 0;
+  // Slot s of block b takes rows b * RPB + s + k * stride; every slot runs
+  // the same trip count so block-wide barriers line up.
+  const int64_t stride = (int64_t)gridDim.x * RPB;
+  const int64_t row0 = (int64_t)blockIdx.x * RPB;
+  const int64_t trips = (rows - row0 + stride - 1) / stride;
 
   Vec<T> xv[VPT], gv[VPT], xn[VPT], gn[VPT];
   auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* go) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int v = lane + k * TPR;
-      if (row < row_end && v < nvec) {
+      if (row < rows && v < nvec) {
         xo[k] = ld16_stream(x + row * cols + v * P);
         go[k] = ld16_stream(dy + row * cols + v * P);
       }
@@ -220,9 +295,9 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
   fetch(row0 + slot, xv, gv);
 
   for (int64_t t = 0; t < trips; ++t) {
-    const int64_t row = row0 + slot + t * RPB;
-    const bool live = row < row_end;
-    fetch(row + RPB, xn, gn);  // next row of this slot, in flight during the reduction
+    const int64_t row = row0 + slot + t * stride;
+    const bool live = row < rows;
+    fetch(row + stride, xn, gn);  // next row of this slot, in flight during the reduction
     const float r = live ? rstd[row] : 0.f;
     float dot = 0.f;
 #pragma unroll
@@ -266,25 +341,23 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
   }
 }
 
-// Any row width: one block walks rows_per_block rows, one column per thread
-// per step, one partial row per block.
+// Any row width: block b walks rows b, b + G, ..., one column per thread per
+// step, one partial row per block.
 template <typename T, bool BIAS>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict__ x, const T* __restrict__ w,
                                                             const float* __restrict__ rstd,
                                                             const T* __restrict__ dy, T* __restrict__ dx,
                                                             float* __restrict__ dw_part,
                                                             float* __restrict__ db_part, int64_t rows, int cols,
-                                                            float inv_cols, int64_t rows_per_block) {
+                                                            float inv_cols) {
   __shared__ float red[kThreads / 64];
-  const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
-  const int64_t row_end = row0 + rows_per_block < rows ? row0 + rows_per_block : rows;
   float* dwp = dw_part + (int64_t)blockIdx.x * cols;
   float* dbp = BIAS ? db_part + (int64_t)blockIdx.x * cols : nullptr;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
     dwp[c] = 0.f;
     if constexpr (BIAS) dbp[c] = 0.f;
   }
-  for (int64_t row = row0; row < row_end; ++row) {
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const float r = rstd[row];
     const T* xr = x + row * cols;
     const T* gr = dy + row * cols;
@@ -397,7 +470,18 @@ template <typename T, bool BIAS, int NTB, int TPR, int VPT>
 void launch_fwd_vec(int64_t rows, const void* x, const void* w, const void* b, void* y, float* rstd, int cols,
                     float eps, hipStream_t s) {
   constexpr int RPB = NTB / TPR;
-  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>), dim3((rows + RPB - 1) / RPB), dim3(NTB), 0, s,
+  const int64_t groups = (rows + RPB - 1) / RPB;
+  // Up to four waves of resident blocks: the persistent grid.
+  static const int per_cu = resident_per_cu(rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>, NTB, 0);
+  static const int per_cu_grid = resident_per_cu(rmsnorm_fwd_grid<T, NTB, TPR, VPT, BIAS>, NTB, 0);
+  if (groups <= (int64_t)4 * cu_count() * per_cu) {
+    const int64_t slots = (int64_t)cu_count() * per_cu_grid;
+    hipLaunchKernelGGL((rmsnorm_fwd_grid<T, NTB, TPR, VPT, BIAS>), dim3(groups < slots ? groups : slots), dim3(NTB), 0,
+                       s, static_cast<const T*>(x), static_cast<const T*>(w), static_cast<const T*>(b),
+                       static_cast<T*>(y), rstd, rows, cols, eps, 1.0f / (float)cols);
+    return;
+  }
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>), dim3(groups), dim3(NTB), 0, s,
                      static_cast<const T*>(x), static_cast<const T*>(w), static_cast<const T*>(b),
                      static_cast<T*>(y), rstd, rows, cols, eps, 1.0f / (float)cols);
 }
@@ -414,11 +498,10 @@ struct BwdArgs {
 
 template <typename T, bool BIAS, int NTB, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
   constexpr int RPB = NTB / TPR;
-  const int64_t per = (a.rows + blocks - 1) / blocks;
   const size_t lds = RPB > 1 ? (size_t)a.cols * sizeof(float) : 0;
   hipLaunchKernelGGL((rmsnorm_bwd_vec<T, NTB, TPR, VPT, BIAS>), dim3(blocks), dim3(NTB), lds, a.s,
                      static_cast<const T*>(a.x), static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy),
-                     static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols, per);
+                     static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
 }
 
 // Every (ntb, tpr, vpt) the planner can return.
@@ -487,12 +570,10 @@ template <typename T, bool BIAS> int bwd(const BwdArgs& a) {
   }
   PK_RMS_BWD_SHAPES(PK_BWD_CASE)
 #undef PK_BWD_CASE
-  if (!done) {
-    const int64_t per = (a.rows + blocks - 1) / blocks;
+  if (!done)
     hipLaunchKernelGGL((rmsnorm_bwd_any<T, BIAS>), dim3(blocks), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
                        static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy), static_cast<T*>(a.dx),
-                       a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols, per);
-  }
+                       a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
   column_sums<T>(a.dw_part, a.stage, static_cast<T*>(a.dw), blocks, a.cols, a.s);
   if (BIAS) column_sums<T>(a.db_part, a.stage, static_cast<T*>(a.db), blocks, a.cols, a.s);
   return launched("pk_rmsnorm_bwd");

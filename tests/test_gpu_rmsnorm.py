@@ -53,8 +53,10 @@ def _run(shape, dtype, eps, with_bias, seed):
         gauge_ok(grads_m[2], db64, grads_r[2], dtype, "db")
 
 
+# (3000, 4096) and (9001, 256) run the persistent forward grid over several
+# row strides with a ragged last stride (one row per block and four per block).
 SHAPES = [(1, 64), (4, 4096), (3, 1000), (17, 8192), (2, 3, 512), (5, 16384), (2, 20000), (300, 128), (1, 7),
-          (3, 3000), (2, 40000), (1030, 2048)]
+          (3, 3000), (2, 40000), (1030, 2048), (3000, 4096), (9001, 256)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=str)
