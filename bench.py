@@ -35,10 +35,19 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "achieved HBM TB/s (norm/rope/swiglu) + attn-fwd bf16 TFLOP/s, % of peak"
 FLUSH_BYTES = 512 << 20  # inputs of a workload are rotated until they exceed the 256 MB MALL twice over
 
-# HBM bytes per launch of each dominant kernel, from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE runs scaled by the same counters' reading for a plain device
-# copy (profiles/hbm_traffic.md). None until measured for that kernel.
-MEASURED_TRAFFIC: dict[str, int | None] = {}
+# HBM bytes per launch of each dominant kernel at its bench workload, from
+# rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by the same counters' reading
+# for a plain device copy of known size (FETCH_SIZE reads half the bytes a
+# copy moves, WRITE_SIZE all of them): 2 * FETCH_SIZE + WRITE_SIZE, in bytes
+# (profiles/hbm_traffic.md). Re-measure after changing a kernel's traffic.
+MEASURED_TRAFFIC: dict[str, int | None] = {
+    "rmsnorm_fwd_grid": 134_549_339,
+    "swiglu_fwd_vec": 1_409_309_330,
+    "rotary_kernel": 539_013_266,
+    "rmsnorm_bwd_vec": 3_240_299_913,
+    "attn_fwd_kernel": 2_632_999_026,
+    "copy": 1_073_766_308,
+}
 
 
 @dataclass
