@@ -5,8 +5,9 @@
 A step is one pass of a workload's drop-in call (the `popcorn_amd.impls`
 function Popcorn dispatches to) over one batch of synthetic input already
 resident in HBM. The default workload is BASELINE config 2 (SwiGLU forward,
-bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, or `copy`, a
-plain device copy of known size used to calibrate HBM byte counters.
+bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, `add_rmsnorm`
+(residual add + RMSNorm at C4's shape, the next op on the norm path), or
+`copy`, a plain device copy of known size used to calibrate HBM byte counters.
 
 Rank 0 prints ONE JSON line. `value` is the workload's achieved algorithmic
 throughput (TB/s of HBM bytes for c1-c4, TFLOP/s for c5). `roofline` is the
@@ -35,17 +36,19 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "achieved HBM TB/s (norm/rope/swiglu) + attn-fwd bf16 TFLOP/s, % of peak"
 FLUSH_BYTES = 512 << 20  # inputs of a workload are rotated until they exceed the 256 MB MALL twice over
 
-# HBM bytes per launch of each dominant kernel at its bench workload, from
-# rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by the same counters' reading
-# for a plain device copy of known size (FETCH_SIZE reads half the bytes a
-# copy moves, WRITE_SIZE all of them): 2 * FETCH_SIZE + WRITE_SIZE, in bytes
-# (profiles/hbm_traffic.md). Re-measure after changing a kernel's traffic.
+# HBM bytes per launch of each workload's dominant kernel, from rocprofv3
+# FETCH_SIZE / WRITE_SIZE runs scaled by the same counters' reading for a plain
+# device copy of known size (FETCH_SIZE reads half the bytes a copy moves,
+# WRITE_SIZE all of them): 2 * FETCH_SIZE + WRITE_SIZE, in bytes
+# (profiles/hbm_traffic.md). Keyed by workload; re-measure after changing a
+# kernel's traffic.
 MEASURED_TRAFFIC: dict[str, int | None] = {
-    "rmsnorm_fwd_grid": 134_549_339,
-    "swiglu_fwd_vec": 1_409_309_330,
-    "rotary_kernel": 539_013_266,
-    "rmsnorm_bwd_vec": 3_240_299_913,
-    "attn_fwd_kernel": 2_632_999_026,
+    "c1": 134_549_339,
+    "c2": 1_409_309_330,
+    "c3": 539_013_266,
+    "c4": 3_240_299_913,
+    "c5": 2_632_999_026,
+    "add_rmsnorm": 4_314_051_694,
     "copy": 1_073_766_308,
 }
 
@@ -223,6 +226,55 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                         step, "rmsnorm_bwd_vec", bwd_bytes, launch,
                         {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu)
 
+    if name == "add_rmsnorm":
+        # not a BASELINE config: the next op on the norm path (residual add + RMSNorm) at C4's shape
+        rows, cols = 65536, 8192
+        x = _randn((rows, cols), torch.bfloat16, gen, dev)
+        res = _randn((rows, cols), torch.bfloat16, gen, dev)
+        w = (1 + 0.1 * _randn((cols,), torch.float32, gen, dev)).bfloat16()
+        dy = _randn((rows, cols), torch.bfloat16, gen, dev)
+        ds = _randn((rows, cols), torch.bfloat16, gen, dev)
+        elems = rows * cols
+        fwd_bytes = 4 * elems * 2 + cols * 2  # read x, residual; write y, s
+        bwd_bytes = 4 * elems * 2 + cols * 2 + cols * 4  # read s, dy, ds; write dx; w; dw
+        xg, rg, wg = (t.detach().requires_grad_() for t in (x, res, w))
+        y, sm, dsum = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+        dw = torch.empty_like(w)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        _lib.check(lib.pk_add_rmsnorm_fwd(x.data_ptr(), res.data_ptr(), w.data_ptr(), y.data_ptr(), sm.data_ptr(),
+                                          rstd.data_ptr(), rows, cols, 1e-6, 1.0, _lib.BF16, stream()))
+        ws_bytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, _lib.BF16)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+
+        def step(i):
+            yy, ss = impls.add_rms_norm(xg, rg, wg, 1e-6, 1.0)
+            torch.autograd.grad((yy, ss), (xg, rg, wg), (dy, ds))
+
+        def launch(i):
+            _lib.check(lib.pk_add_rmsnorm_bwd(sm.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(),
+                                              ds.data_ptr(), dsum.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws_bytes,
+                                              rows, cols, 1.0, _lib.BF16, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            sample = 2048
+            xc, rc = (torch.randn(sample, cols).bfloat16().requires_grad_() for _ in range(2))
+            wc = (1 + 0.1 * torch.randn(cols)).bfloat16().requires_grad_()
+            gc, sc = torch.randn(sample, cols).bfloat16(), torch.randn(sample, cols).bfloat16()
+
+            def one():
+                yc, s_c = R.add_rms_norm(xc, rc, wc, 1e-6, 1.0)
+                torch.autograd.grad((yc, s_c), (xc, rc, wc), (gc, sc))
+
+            t, reps = _time_cpu(one)
+            work = 8 * sample * cols * 2 + 2 * cols * 2 + cols * 4
+            return work / t / 1e12, f"{sample} of {rows} rows x {cols} bf16, fwd+bwd, median of {reps} reps"
+
+        return Workload("add_rmsnorm", "add_rms_norm fwd+bwd bf16 x, residual, dy, ds [65536, 8192], offset 1",
+                        "bf16", "TB/s", fwd_bytes + bwd_bytes, step, "rmsnorm_bwd_vec", bwd_bytes, launch,
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu)
+
     if name == "c5":
         B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
         q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
@@ -269,7 +321,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         return Workload("copy", "plain device copy, 512 MiB -> 512 MiB", "bf16", "TB/s", nbytes, step, "copy",
                         nbytes, step, {"bytes_each_way": numel * 2})
 
-    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, copy)")
+    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, copy)")
 
 
 def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 20) -> tuple[float, int]:
@@ -322,7 +374,7 @@ def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
         "frac": round(achieved / peak, 4),
         "avg_launch_us": round(avg * 1e3, 2),
         "work_per_launch": wl.kernel_work,
-        "traffic": MEASURED_TRAFFIC.get(wl.kernel),
+        "traffic": MEASURED_TRAFFIC.get(wl.name),
     }
 
 
@@ -345,7 +397,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
     args = ap.parse_args(argv)
@@ -372,7 +424,7 @@ def main(argv=None) -> int:
 
     others = {}
     if not args.no_others and wl.name != "copy":
-        for name in ("c1", "c2", "c3", "c4", "c5"):
+        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm"):
             if name == wl.name:
                 continue
             del wl

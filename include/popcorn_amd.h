@@ -71,7 +71,7 @@ int pk_swiglu_bwd(const void* dy, const void* a, const void* b, void* da, void* 
 int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, float* rstd, int64_t rows, int64_t cols,
                    float eps, int dtype, void* stream);
 
-/* Bytes of device workspace pk_rmsnorm_bwd needs for this shape. */
+/* Bytes of device workspace pk_rmsnorm_bwd and pk_add_rmsnorm_bwd need for this shape. */
 int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
 
 /*
@@ -84,6 +84,29 @@ int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
  */
 int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
                    void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream);
+
+/*
+ * Residual add fused with RMSNorm, over `rows` contiguous rows of `cols`:
+ *   s = round(x + residual); r = 1/sqrt(mean(s^2) + eps);
+ *   y = round(round(s*r) * round(w + offset)).
+ * Writes y and s (the new residual stream); rstd (fp32 [rows]) may be NULL.
+ * All tensors share `dtype`. Replaces: reference `add_rms_norm`
+ * (kernels/add_rms_norm.py:8-26, `s = x + residual; rms(s, eps) * (weight + offset)`).
+ */
+int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y, void* s, float* rstd,
+                       int64_t rows, int64_t cols, float eps, float offset, int dtype, void* stream);
+
+/*
+ * Backward of pk_add_rmsnorm_fwd. With n = s*r, u = dy*(w + offset):
+ *   ds_total = r*(u - n*mean(u*n)) + ds,  dw = sum_rows dy*n,
+ * where ds is the gradient reaching s through the second output (may be
+ * NULL). ds_total is the gradient of both x and residual (dx). The workspace
+ * is sized by pk_rmsnorm_bwd_workspace. Replaces torch autograd of the
+ * reference (kernels/add_rms_norm.py:25-26).
+ */
+int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const void* dy, const void* ds, void* dx,
+                       void* dw, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, float offset,
+                       int dtype, void* stream);
 
 /*
  * Rotary embedding of x [batch, seq, heads, head_dim] with tables

@@ -18,6 +18,10 @@ independent fact that a plausible slip would break:
                     scale invariance; zero row -> 0
   rms_norm_bwd      float64 autograd of F.rms_norm; central finite differences;
                     <dx, x> = 0 when w = 1, eps = 0; dw = sum dy*n
+  add_rms_norm      float64 F.rms_norm of x + residual with weight + offset;
+                    residual = 0, offset = 0 reduces to rms_norm
+  add_rms_norm_bwd  float64 autograd through both outputs (y and s); central
+                    finite differences; d(x) = d(residual)
   swiglu            scipy.special.expit formulation; silu(0) = 0; silu(x) -> x
   swiglu_bwd        central finite differences; float64 autograd of F.silu
   rotary_embedding  complex multiplication (x1 + i x2)(c + i s); identity tables;
@@ -34,6 +38,8 @@ import numpy as np
 __all__ = [
     "rms_norm",
     "rms_norm_bwd",
+    "add_rms_norm",
+    "add_rms_norm_bwd",
     "swiglu",
     "swiglu_bwd",
     "rotary_embedding",
@@ -72,6 +78,30 @@ def rms_norm_bwd(x, weight, dy, eps: float = 1e-6):
     dx = r * (u - n * np.mean(u * n, axis=-1, keepdims=True))
     lead = tuple(range(x.ndim - 1))
     return dx, np.sum(g * n, axis=lead), np.sum(g, axis=lead)
+
+
+def add_rms_norm(x, residual, weight, eps: float = 1e-6, offset: float = 0.0):
+    """(y, s) with s = x + residual and y = s * rsqrt(mean(s^2, -1) + eps) * (weight + offset).
+
+    Follows kernels/add_rms_norm.py:25-26 (`s = x + residual`,
+    `rms(s, eps) * (weight + offset)`, returning (y, s)).
+    """
+    s = _f64(x) + _f64(residual)
+    return rms_norm(s, _f64(weight) + offset, None, eps), s
+
+
+def add_rms_norm_bwd(x, residual, weight, dy, ds=None, eps: float = 1e-6, offset: float = 0.0):
+    """Gradients of `add_rms_norm` for cotangents dy (of y) and ds (of s, or None):
+    (dx, dresidual, dweight).
+
+    The sum s feeds both outputs, so its gradient is the RMSNorm input gradient
+    (with weight + offset) plus ds, and x and residual each receive it.
+    """
+    s = _f64(x) + _f64(residual)
+    dsum, dw, _ = rms_norm_bwd(s, _f64(weight) + offset, dy, eps)
+    if ds is not None:
+        dsum = dsum + _f64(ds)
+    return dsum, dsum.copy(), dw
 
 
 def _sigmoid(a: np.ndarray) -> np.ndarray:

@@ -58,6 +58,16 @@ def rms_norm_supported(x, weight, bias, eps) -> bool:
     )
 
 
+def add_rms_norm_supported(x, residual, weight, eps, offset) -> bool:
+    return (
+        _on_hip(x, residual, weight)
+        and x.dtype == residual.dtype == weight.dtype
+        and x.dtype in _FLOATS
+        and x.shape == residual.shape
+        and x.shape[-1] > 0
+    )
+
+
 def swiglu_supported(a, b) -> bool:
     return _on_hip(a, b) and a.dtype == b.dtype and a.dtype in _FLOATS and a.shape == b.shape
 
@@ -88,6 +98,7 @@ def attn_supported(q, k, v, causal, softmax_scale) -> bool:
 # so Popcorn declines it whenever a call needs gradients.
 REGISTRATIONS = (
     ("rms_norm", "popcorn_amd.impls.rms_norm", rms_norm_supported, False),
+    ("add_rms_norm", "popcorn_amd.impls.add_rms_norm", add_rms_norm_supported, False),
     ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
     ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
     ("attn", "popcorn_amd.impls.attn", attn_supported, True),
@@ -107,7 +118,7 @@ def _popcorn() -> ModuleType:
 
 
 def register(popcorn: ModuleType | None = None) -> ModuleType:
-    """Declare the backend and register the four ops on `popcorn` (default: the real package, else compat)."""
+    """Declare the backend and register its ops on `popcorn` (default: the real package, else compat)."""
     pc = popcorn if popcorn is not None else _popcorn()
     pc.declare_backend(BACKEND, package=DISTRIBUTION, min_version=__version__, max_version=__version__)
     for op_name, source, predicate, forward_only in REGISTRATIONS:

@@ -1,7 +1,7 @@
-"""The four transformer-block ops, registered with their torch references.
+"""The transformer-block ops, registered with their torch references.
 
 Signatures, shape annotations and test-argument pools are Popcorn's
-(kernels/rms_norm.py:16-30, kernels/swiglu.py:9-18,
+(kernels/rms_norm.py:16-30, kernels/add_rms_norm.py:8-26, kernels/swiglu.py:9-18,
 kernels/rotary_embedding.py:12-40, kernels/attn.py:10-37); the arithmetic is
 the eager-torch restatement in `popcorn_amd.compat.references`.
 """
@@ -22,6 +22,18 @@ def rms_norm(
 ) -> Float[Tensor, "... normalized_shape"]:
     """Root-mean-square normalization: x * rsqrt(mean(x^2) + eps) * weight (+ bias)."""
     return references.rms_norm(x, weight, bias, eps)
+
+
+@register_kernel(test_args={"eps": [1e-6, 1e-5], "offset": [0.0, 1.0]})
+def add_rms_norm(
+    x: Float[Tensor, "... hidden"],
+    residual: Float[Tensor, "... hidden"],
+    weight: Float[Tensor, "hidden"],
+    eps: float = 1e-6,
+    offset: float = 0.0,
+) -> tuple[Tensor, Tensor]:
+    """Residual add fused with RMS norm: (rms(x + residual) * (weight + offset), x + residual)."""
+    return references.add_rms_norm(x, residual, weight, eps, offset)
 
 
 @register_kernel

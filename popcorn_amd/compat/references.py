@@ -7,6 +7,7 @@ eager torch with the same sequence of tensor ops, because that sequence fixes
 the native-dtype rounding the budget measures:
 
     rms_norm          kernels/rms_norm.py:16-30 (`rms`, `upcast`: kernels/_utils.py:6-16)
+    add_rms_norm      kernels/add_rms_norm.py:8-26
     swiglu            kernels/swiglu.py:9-18
     rotary_embedding  kernels/rotary_embedding.py:12-40
     attn              kernels/attn.py:10-37
@@ -30,6 +31,15 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
     inv_rms = torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)
     y = (h * inv_rms).to(x.dtype) * weight
     return y if bias is None else y + bias
+
+
+def add_rms_norm(x: Tensor, residual: Tensor, weight: Tensor, eps: float = 1e-6,
+                 offset: float = 0.0) -> tuple[Tensor, Tensor]:
+    """s = x + residual at the inputs' dtype; (rms(s) rounded to that dtype) * (weight + offset); returns (y, s)."""
+    s = x + residual
+    h = upcast(s)
+    normed = (h * torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)).to(s.dtype)
+    return normed * (weight + offset), s
 
 
 def swiglu(a: Tensor, b: Tensor) -> Tensor:

@@ -21,6 +21,8 @@
 // Blocks leave one fp32 partial row each (the rows of a block's wavefront
 // slots are combined through LDS first), and a two-stage column reduction
 // sums the partials in a fixed order, so dw is deterministic.
+#include <math.h>
+
 #include "api.h"
 #include "common.h"
 
@@ -52,6 +54,22 @@ template <int NTB, int TPR> __device__ __forceinline__ float row_sum(float v, fl
 }
 
 // torch: rms = (h * rsqrt(mean(h^2) + eps)).to(T); y = rms * w; y = y + bias.
+// Kernel modes: the plain norm, the norm plus bias, and the residual-add form
+// (s = x + residual is formed, written out and normalised, with weight + offset).
+constexpr int kPlain = 0, kBias = 1, kAdd = 2;
+
+// s = round(x + residual): the sum torch forms at T before normalising it
+template <typename T> __device__ __forceinline__ void add_residual(Vec<T>& xv, const Vec<T>& rv) {
+#pragma unroll
+  for (int j = 0; j < Vec<T>::N; ++j) xv.v[j] = from_f32<T>(to_f32(xv.v[j]) + to_f32(rv.v[j]));
+}
+// w + offset, rounded to T like the reference's `weight + offset`
+template <typename T> __device__ __forceinline__ Vec<T> offset_weight(Vec<T> wv, float offset) {
+#pragma unroll
+  for (int j = 0; j < Vec<T>::N; ++j) wv.v[j] = from_f32<T>(to_f32(wv.v[j]) + offset);
+  return wv;
+}
+
 template <typename T, bool BIAS> __device__ __forceinline__ T fwd_elem(float xv, float r, float wv, float bv) {
   float y = round_to<T>(xv * r) * wv;
   if constexpr (BIAS) y = round_to<T>(y) + bv;
@@ -59,11 +77,13 @@ template <typename T, bool BIAS> __device__ __forceinline__ T fwd_elem(float xv,
 }
 
 // One row per TPR lanes, RPB = NTB / TPR rows per block.
-template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+template <typename T, int NTB, int TPR, int VPT, int MODE>
 __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, const T* __restrict__ w,
-                                                       const T* __restrict__ bias, T* __restrict__ y,
+                                                       const T* __restrict__ bias, const T* __restrict__ res,
+                                                       T* __restrict__ s_out, float offset, T* __restrict__ y,
                                                        float* __restrict__ rstd, int64_t rows, int cols, float eps,
                                                        float inv_cols) {
+  constexpr bool BIAS = MODE == kBias;
   constexpr int P = Vec<T>::N;
   constexpr int RPB = NTB / TPR;
   __shared__ float red[NTB / 64];
@@ -80,6 +100,10 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
     const int v = lane + k * TPR;
     if (live && v < nvec) {
       xv[k] = ld16_stream(xr + v * P);
+      if constexpr (MODE == kAdd) {
+        add_residual(xv[k], ld16_stream(res + row * cols + v * P));
+        st16_stream(s_out + row * cols + v * P, xv[k]);
+      }
 #pragma unroll
       for (int j = 0; j < P; ++j) {
         const float f = to_f32(xv[k].v[j]);
@@ -97,7 +121,8 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
   for (int k = 0; k < VPT; ++k) {
     const int v = lane + k * TPR;
     if (v < nvec) {
-      const Vec<T> wv = ld16(w + v * P);
+      Vec<T> wv = ld16(w + v * P);
+      if constexpr (MODE == kAdd) wv = offset_weight(wv, offset);
       Vec<T> bv;
       if constexpr (BIAS) bv = ld16(bias + v * P);
       Vec<T> out;
@@ -112,11 +137,13 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
 // Persistent form of rmsnorm_fwd_vec for short launches: slot s of block b
 // takes rows b * RPB + s + k * stride, with w (and bias) in registers and the
 // next row's x in flight while the current row is reduced.
-template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+template <typename T, int NTB, int TPR, int VPT, int MODE>
 __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x, const T* __restrict__ w,
-                                                        const T* __restrict__ bias, T* __restrict__ y,
+                                                        const T* __restrict__ bias, const T* __restrict__ res,
+                                                        T* __restrict__ s_out, float offset, T* __restrict__ y,
                                                         float* __restrict__ rstd, int64_t rows, int cols, float eps,
                                                         float inv_cols) {
+  constexpr bool BIAS = MODE == kBias;
   constexpr int P = Vec<T>::N;
   constexpr int RPB = NTB / TPR;
   __shared__ float red[NTB / 64];
@@ -132,31 +159,41 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x,
     const int v = lane + k * TPR;
     if (v < nvec) {
       wv[k] = ld16(w + v * P);
+      if constexpr (MODE == kAdd) wv[k] = offset_weight(wv[k], offset);
       if constexpr (BIAS) bv[k] = ld16(bias + v * P);
     }
   }
   Vec<T> xv[VPT], xn[VPT];
-  auto fetch = [&](int64_t row, Vec<T>* xo) {
+  Vec<T> rv[MODE == kAdd ? VPT : 1], rn[MODE == kAdd ? VPT : 1];
+  auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* ro) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int v = lane + k * TPR;
-      if (row < rows && v < nvec) xo[k] = ld16_stream(x + row * cols + v * P);
+      if (row < rows && v < nvec) {
+        xo[k] = ld16_stream(x + row * cols + v * P);
+        if constexpr (MODE == kAdd) ro[k] = ld16_stream(res + row * cols + v * P);
+      }
     }
   };
-  fetch(row0, xv);
+  fetch(row0, xv, rv);
   for (int64_t t = 0; t < trips; ++t) {
     const int64_t row = row0 + t * stride;
-    fetch(row + stride, xn);
+    fetch(row + stride, xn, rn);
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int v = lane + k * TPR;
-      if (row < rows && v < nvec)
+      if (row < rows && v < nvec) {
+        if constexpr (MODE == kAdd) {
+          add_residual(xv[k], rv[k]);
+          st16_stream(s_out + row * cols + v * P, xv[k]);
+        }
 #pragma unroll
         for (int j = 0; j < P; ++j) {
           const float f = to_f32(xv[k].v[j]);
           ss += f * f;
         }
+      }
     }
     ss = row_sum<NTB, TPR>(ss, red);
     if (row < rows) {
@@ -175,30 +212,43 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x,
       }
     }
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) xv[k] = xn[k];
+    for (int k = 0; k < VPT; ++k) {
+      xv[k] = xn[k];
+      if constexpr (MODE == kAdd) rv[k] = rn[k];
+    }
   }
 }
 
 // Any row width, any alignment: one block per row, two passes over x.
-template <typename T, bool BIAS>
+template <typename T, int MODE>
 __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict__ x, const T* __restrict__ w,
-                                                            const T* __restrict__ bias, T* __restrict__ y,
+                                                            const T* __restrict__ bias, const T* __restrict__ res,
+                                                            T* __restrict__ s_out, float offset, T* __restrict__ y,
                                                             float* __restrict__ rstd, int64_t rows, int cols,
                                                             float eps, float inv_cols) {
+  constexpr bool BIAS = MODE == kBias;
   __shared__ float red[kThreads / 64];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
   float ss = 0.f;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float f = to_f32(xr[c]);
+    float f = to_f32(xr[c]);
+    if constexpr (MODE == kAdd) {
+      const T sv = from_f32<T>(f + to_f32(res[row * cols + c]));
+      s_out[row * cols + c] = sv;  // re-read below by this same thread
+      f = to_f32(sv);
+    }
     ss += f * f;
   }
   ss = row_sum<kThreads, kThreads>(ss, red);
   const float r = 1.0f / sqrtf(ss * inv_cols + eps);
   if (rstd != nullptr && threadIdx.x == 0) rstd[row] = r;
   T* yr = y + row * cols;
-  for (int c = threadIdx.x; c < cols; c += kThreads)
-    yr[c] = fwd_elem<T, BIAS>(to_f32(xr[c]), r, to_f32(w[c]), BIAS ? to_f32(bias[c]) : 0.f);
+  const T* sr = MODE == kAdd ? s_out + row * cols : xr;
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    const float wv = MODE == kAdd ? to_f32(from_f32<T>(to_f32(w[c]) + offset)) : to_f32(w[c]);
+    yr[c] = fwd_elem<T, BIAS>(to_f32(sr[c]), r, wv, BIAS ? to_f32(bias[c]) : 0.f);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -247,12 +297,17 @@ __device__ __forceinline__ void flush_partial(float (&acc)[VPT][P], float* lds_r
   }
 }
 
-template <typename T, int NTB, int TPR, int VPT, bool BIAS>
+// MODE kAdd: x is the residual sum s, w is used as w + offset, and ds (the
+// gradient reaching s from its second use, may be NULL) is added to dx.
+template <typename T, int NTB, int TPR, int VPT, int MODE>
 __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, const T* __restrict__ w,
                                                        const float* __restrict__ rstd, const T* __restrict__ dy,
-                                                       T* __restrict__ dx, float* __restrict__ dw_part,
-                                                       float* __restrict__ db_part, int64_t rows, int cols,
-                                                       float inv_cols) {
+                                                       const T* __restrict__ ds, float offset, T* __restrict__ dx,
+                                                       float* __restrict__ dw_part, float* __restrict__ db_part,
+                                                       int64_t rows, int cols, float inv_cols) {
+  constexpr bool BIAS = MODE == kBias;
+  constexpr bool ADD = MODE == kAdd;
+  const bool has_ds = ADD && ds != nullptr;
   constexpr int P = Vec<T>::N;
   constexpr int RPB = NTB / TPR;
   __shared__ float red[NTB / 64];
@@ -267,6 +322,7 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
     const int v = lane + k * TPR;
     Vec<T> wv;
     if (v < nvec) wv = ld16(w + v * P);
+    if constexpr (ADD) wv = offset_weight(wv, offset);
 #pragma unroll
     for (int j = 0; j < P; ++j) {
       wf[k][j] = v < nvec ? to_f32(wv.v[j]) : 0.f;
@@ -282,22 +338,24 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
   const int64_t trips = (rows - row0 + stride - 1) / stride;
 
   Vec<T> xv[VPT], gv[VPT], xn[VPT], gn[VPT];
-  auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* go) {
+  Vec<T> sv[ADD ? VPT : 1], sn[ADD ? VPT : 1];
+  auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* go, Vec<T>* so) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int v = lane + k * TPR;
       if (row < rows && v < nvec) {
         xo[k] = ld16_stream(x + row * cols + v * P);
         go[k] = ld16_stream(dy + row * cols + v * P);
+        if (has_ds) so[k] = ld16_stream(ds + row * cols + v * P);
       }
     }
   };
-  fetch(row0 + slot, xv, gv);
+  fetch(row0 + slot, xv, gv, sv);
 
   for (int64_t t = 0; t < trips; ++t) {
     const int64_t row = row0 + slot + t * stride;
     const bool live = row < rows;
-    fetch(row + stride, xn, gn);  // next row of this slot, in flight during the reduction
+    fetch(row + stride, xn, gn, sn);  // next row of this slot, in flight during the reduction
     const float r = live ? rstd[row] : 0.f;
     float dot = 0.f;
 #pragma unroll
@@ -319,7 +377,9 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
           for (int j = 0; j < P; ++j) {
             const float g = to_f32(gv[k].v[j]);
             const float n = to_f32(xv[k].v[j]) * r;
-            out.v[j] = from_f32<T>(r * (g * wf[k][j] - n * dot));
+            float d = r * (g * wf[k][j] - n * dot);
+            if constexpr (ADD) d += has_ds ? to_f32(sv[k].v[j]) : 0.f;
+            out.v[j] = from_f32<T>(d);
             dwa[k][j] += g * n;
             if constexpr (BIAS) dba[k][j] += g;
           }
@@ -331,6 +391,7 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
     for (int k = 0; k < VPT; ++k) {
       xv[k] = xn[k];
       gv[k] = gn[k];
+      if constexpr (ADD) sv[k] = sn[k];
     }
   }
 
@@ -343,13 +404,19 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
 
 // Any row width: block b walks rows b, b + G, ..., one column per thread per
 // step, one partial row per block.
-template <typename T, bool BIAS>
+template <typename T, int MODE>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict__ x, const T* __restrict__ w,
                                                             const float* __restrict__ rstd,
-                                                            const T* __restrict__ dy, T* __restrict__ dx,
+                                                            const T* __restrict__ dy, const T* __restrict__ ds,
+                                                            float offset, T* __restrict__ dx,
                                                             float* __restrict__ dw_part,
                                                             float* __restrict__ db_part, int64_t rows, int cols,
                                                             float inv_cols) {
+  constexpr bool BIAS = MODE == kBias;
+  constexpr bool ADD = MODE == kAdd;
+  const bool has_ds = ADD && ds != nullptr;
+  // weight as the forward used it: w, or w + offset rounded to T
+  auto wc = [&](int c) { return ADD ? to_f32(from_f32<T>(to_f32(w[c]) + offset)) : to_f32(w[c]); };
   __shared__ float red[kThreads / 64];
   float* dwp = dw_part + (int64_t)blockIdx.x * cols;
   float* dbp = BIAS ? db_part + (int64_t)blockIdx.x * cols : nullptr;
@@ -362,13 +429,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
     const T* xr = x + row * cols;
     const T* gr = dy + row * cols;
     float dot = 0.f;
-    for (int c = threadIdx.x; c < cols; c += kThreads) dot += to_f32(gr[c]) * to_f32(w[c]) * (to_f32(xr[c]) * r);
+    for (int c = threadIdx.x; c < cols; c += kThreads) dot += to_f32(gr[c]) * wc(c) * (to_f32(xr[c]) * r);
     dot = row_sum<kThreads, kThreads>(dot, red) * inv_cols;
     T* dxr = dx + row * cols;
     for (int c = threadIdx.x; c < cols; c += kThreads) {
       const float g = to_f32(gr[c]);
       const float n = to_f32(xr[c]) * r;
-      dxr[c] = from_f32<T>(r * (g * to_f32(w[c]) - n * dot));
+      float d = r * (g * wc(c) - n * dot);
+      if (has_ds) d += to_f32(ds[row * cols + c]);
+      dxr[c] = from_f32<T>(d);
       dwp[c] += g * n;  // column c is only ever touched by this thread
       if constexpr (BIAS) dbp[c] += g;
     }
@@ -453,41 +522,52 @@ template <typename K> int resident_per_cu(K kernel, int threads, size_t lds) {
   return n;
 }
 
-template <typename T, bool BIAS, int NTB, int TPR, int VPT> int bwd_resident(int cols) {
+template <typename T, int MODE, int NTB, int TPR, int VPT> int bwd_resident() {
   // dynamic LDS of a 4-rows-per-block shape: one fp32 row of at most 64*4*8 columns
-  static const int n = resident_per_cu(rmsnorm_bwd_vec<T, NTB, TPR, VPT, BIAS>, NTB,
+  static const int n = resident_per_cu(rmsnorm_bwd_vec<T, NTB, TPR, VPT, MODE>, NTB,
                                        NTB / TPR > 1 ? (size_t)64 * 4 * 8 * sizeof(float) : 0);
-  (void)cols;
   return n;
 }
 
-template <typename T, bool BIAS> int bwd_any_resident() {
-  static const int n = resident_per_cu(rmsnorm_bwd_any<T, BIAS>, kThreads, 0);
+template <typename T, int MODE> int bwd_any_resident() {
+  static const int n = resident_per_cu(rmsnorm_bwd_any<T, MODE>, kThreads, 0);
   return n;
 }
 
-template <typename T, bool BIAS, int NTB, int TPR, int VPT>
-void launch_fwd_vec(int64_t rows, const void* x, const void* w, const void* b, void* y, float* rstd, int cols,
-                    float eps, hipStream_t s) {
+struct FwdArgs {
+  const void *x, *w, *b, *res;
+  void* s_out;
+  float offset;
+  void* y;
+  float* rstd;
+  int64_t rows;
+  int cols;
+  float eps;
+  hipStream_t s;
+};
+
+template <typename T, int MODE, int NTB, int TPR, int VPT> void launch_fwd_vec(const FwdArgs& a) {
   constexpr int RPB = NTB / TPR;
-  const int64_t groups = (rows + RPB - 1) / RPB;
+  const int64_t groups = (a.rows + RPB - 1) / RPB;
+  const T *x = static_cast<const T*>(a.x), *w = static_cast<const T*>(a.w), *b = static_cast<const T*>(a.b),
+          *res = static_cast<const T*>(a.res);
+  T *s_out = static_cast<T*>(a.s_out), *y = static_cast<T*>(a.y);
   // Up to four waves of resident blocks: the persistent grid.
-  static const int per_cu = resident_per_cu(rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>, NTB, 0);
-  static const int per_cu_grid = resident_per_cu(rmsnorm_fwd_grid<T, NTB, TPR, VPT, BIAS>, NTB, 0);
+  static const int per_cu = resident_per_cu(rmsnorm_fwd_vec<T, NTB, TPR, VPT, MODE>, NTB, 0);
+  static const int per_cu_grid = resident_per_cu(rmsnorm_fwd_grid<T, NTB, TPR, VPT, MODE>, NTB, 0);
   if (groups <= (int64_t)4 * cu_count() * per_cu) {
     const int64_t slots = (int64_t)cu_count() * per_cu_grid;
-    hipLaunchKernelGGL((rmsnorm_fwd_grid<T, NTB, TPR, VPT, BIAS>), dim3(groups < slots ? groups : slots), dim3(NTB), 0,
-                       s, static_cast<const T*>(x), static_cast<const T*>(w), static_cast<const T*>(b),
-                       static_cast<T*>(y), rstd, rows, cols, eps, 1.0f / (float)cols);
+    hipLaunchKernelGGL((rmsnorm_fwd_grid<T, NTB, TPR, VPT, MODE>), dim3(groups < slots ? groups : slots), dim3(NTB), 0,
+                       a.s, x, w, b, res, s_out, a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
     return;
   }
-  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, BIAS>), dim3(groups), dim3(NTB), 0, s,
-                     static_cast<const T*>(x), static_cast<const T*>(w), static_cast<const T*>(b),
-                     static_cast<T*>(y), rstd, rows, cols, eps, 1.0f / (float)cols);
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, MODE>), dim3(groups), dim3(NTB), 0, a.s, x, w, b, res, s_out,
+                     a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
 }
 
 struct BwdArgs {
-  const void *x, *w, *dy;
+  const void *x, *w, *dy, *ds;
+  float offset;
   const float* rstd;
   void *dx, *dw, *db;
   float *dw_part, *db_part, *stage;
@@ -496,12 +576,13 @@ struct BwdArgs {
   hipStream_t s;
 };
 
-template <typename T, bool BIAS, int NTB, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
+template <typename T, int MODE, int NTB, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
   constexpr int RPB = NTB / TPR;
   const size_t lds = RPB > 1 ? (size_t)a.cols * sizeof(float) : 0;
-  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, NTB, TPR, VPT, BIAS>), dim3(blocks), dim3(NTB), lds, a.s,
+  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, NTB, TPR, VPT, MODE>), dim3(blocks), dim3(NTB), lds, a.s,
                      static_cast<const T*>(a.x), static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy),
-                     static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
+                     static_cast<const T*>(a.ds), a.offset, static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows,
+                     a.cols, 1.0f / (float)a.cols);
 }
 
 // Every (ntb, tpr, vpt) the planner can return.
@@ -510,39 +591,39 @@ template <typename T, bool BIAS, int NTB, int TPR, int VPT> void launch_bwd_vec(
 #define PK_RMS_BWD_SHAPES(X) X(256, 64, 1) X(256, 64, 2) X(256, 64, 4) X(256, 256, 2) X(512, 512, 2) \
   X(1024, 1024, 2) X(1024, 1024, 4) X(1024, 1024, 8) X(1024, 1024, 16)
 
-template <typename T, bool BIAS>
-int fwd(const void* x, const void* w, const void* b, void* y, float* rstd, int64_t rows, int64_t cols, float eps,
-        hipStream_t s) {
-  const bool aligned = aligned16(x) && aligned16(w) && aligned16(y) && (!BIAS || aligned16(b));
-  const Plan p = plan_for(cols, sizeof(T), aligned, false);
+template <typename T, int MODE> int fwd(const FwdArgs& a, const char* who) {
+  const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.y) && (MODE != kBias || aligned16(a.b)) &&
+                       (MODE != kAdd || (aligned16(a.res) && aligned16(a.s_out)));
+  const Plan p = plan_for(a.cols, sizeof(T), aligned, false);
   bool done = false;
 #define PK_FWD_CASE(NTB, TPR, VPT)                                                         \
   if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
-    launch_fwd_vec<T, BIAS, NTB, TPR, VPT>(rows, x, w, b, y, rstd, (int)cols, eps, s);    \
+    launch_fwd_vec<T, MODE, NTB, TPR, VPT>(a);                                            \
     done = true;                                                                           \
   }
   PK_RMS_FWD_SHAPES(PK_FWD_CASE)
 #undef PK_FWD_CASE
   if (!done)
-    hipLaunchKernelGGL((rmsnorm_fwd_any<T, BIAS>), dim3(rows), dim3(kThreads), 0, s, static_cast<const T*>(x),
-                       static_cast<const T*>(w), static_cast<const T*>(b), static_cast<T*>(y), rstd, rows,
-                       (int)cols, eps, 1.0f / (float)cols);
-  return launched("pk_rmsnorm_fwd");
+    hipLaunchKernelGGL((rmsnorm_fwd_any<T, MODE>), dim3(a.rows), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
+                       static_cast<const T*>(a.w), static_cast<const T*>(a.b), static_cast<const T*>(a.res),
+                       static_cast<T*>(a.s_out), a.offset, static_cast<T*>(a.y), a.rstd, a.rows, a.cols, a.eps,
+                       1.0f / (float)a.cols);
+  return launched(who);
 }
 
 // Persistent backward grid: every resident block slot of the device, never
 // more blocks than the rows need.
-template <typename T, bool BIAS> int64_t bwd_blocks(int64_t rows, const Plan& p) {
+template <typename T, int MODE> int64_t bwd_blocks(int64_t rows, const Plan& p) {
   int per_cu = 0;
   int64_t rpb = 1;
 #define PK_RES_CASE(NTB, TPR, VPT)                                                         \
   if (!per_cu && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                 \
-    per_cu = bwd_resident<T, BIAS, NTB, TPR, VPT>(0);                                     \
+    per_cu = bwd_resident<T, MODE, NTB, TPR, VPT>();                                      \
     rpb = NTB / TPR;                                                                       \
   }
   PK_RMS_BWD_SHAPES(PK_RES_CASE)
 #undef PK_RES_CASE
-  if (!per_cu) per_cu = bwd_any_resident<T, BIAS>();
+  if (!per_cu) per_cu = bwd_any_resident<T, MODE>();
   const int64_t want = (rows + rpb - 1) / rpb;
   const int64_t cap = (int64_t)cu_count() * per_cu;
   return want < cap ? want : cap;
@@ -558,25 +639,26 @@ template <typename T> void column_sums(const float* part, float* stage, T* out, 
   hipLaunchKernelGGL(column_sum_final<T>, dim3(cx), dim3(kThreads), 0, s, stage, out, n, cols);
 }
 
-template <typename T, bool BIAS> int bwd(const BwdArgs& a) {
-  const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.dy) && aligned16(a.dx);
+template <typename T, int MODE> int bwd(const BwdArgs& a, const char* who) {
+  const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.dy) && aligned16(a.dx) &&
+                       (a.ds == nullptr || aligned16(a.ds));
   const Plan p = plan_for(a.cols, sizeof(T), aligned, true);
-  const int64_t blocks = bwd_blocks<T, BIAS>(a.rows, p);
+  const int64_t blocks = bwd_blocks<T, MODE>(a.rows, p);
   bool done = false;
 #define PK_BWD_CASE(NTB, TPR, VPT)                                                         \
   if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
-    launch_bwd_vec<T, BIAS, NTB, TPR, VPT>(a, blocks);                                    \
+    launch_bwd_vec<T, MODE, NTB, TPR, VPT>(a, blocks);                                    \
     done = true;                                                                           \
   }
   PK_RMS_BWD_SHAPES(PK_BWD_CASE)
 #undef PK_BWD_CASE
   if (!done)
-    hipLaunchKernelGGL((rmsnorm_bwd_any<T, BIAS>), dim3(blocks), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
-                       static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy), static_cast<T*>(a.dx),
-                       a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
+    hipLaunchKernelGGL((rmsnorm_bwd_any<T, MODE>), dim3(blocks), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
+                       static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy), static_cast<const T*>(a.ds),
+                       a.offset, static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
   column_sums<T>(a.dw_part, a.stage, static_cast<T*>(a.dw), blocks, a.cols, a.s);
-  if (BIAS) column_sums<T>(a.db_part, a.stage, static_cast<T*>(a.db), blocks, a.cols, a.s);
-  return launched("pk_rmsnorm_bwd");
+  if (MODE == kBias) column_sums<T>(a.db_part, a.stage, static_cast<T*>(a.db), blocks, a.cols, a.s);
+  return launched(who);
 }
 
 // Workspace: [blocks, cols] dw partials, the same for dbias, and the
@@ -585,25 +667,71 @@ struct Layout {
   int64_t part, stage, total;
 };
 
-template <typename T, bool BIAS> Layout layout_for(int64_t rows, int64_t cols) {
+template <typename T, int MODE> Layout layout_for(int64_t rows, int64_t cols) {
   // The aligned plan and the fallback may use different grids: size for the larger.
-  const int64_t b1 = bwd_blocks<T, BIAS>(rows, plan_for(cols, sizeof(T), true, true));
-  const int64_t b2 = bwd_blocks<T, BIAS>(rows, plan_for(cols, sizeof(T), false, true));
+  const int64_t b1 = bwd_blocks<T, MODE>(rows, plan_for(cols, sizeof(T), true, true));
+  const int64_t b2 = bwd_blocks<T, MODE>(rows, plan_for(cols, sizeof(T), false, true));
   const int64_t blocks = b1 > b2 ? b1 : b2;
   auto up = [](int64_t n) { return (n + 255) / 256 * 256; };
   Layout l;
   l.part = up(blocks * cols * (int64_t)sizeof(float));
   l.stage = up(stage_rows(blocks) * cols * (int64_t)sizeof(float));
-  l.total = l.part * (BIAS ? 2 : 1) + l.stage;
+  l.total = l.part * (MODE == kBias ? 2 : 1) + l.stage;
   return l;
 }
 
-Layout workspace_layout(int64_t rows, int64_t cols, int dtype, bool bias) {
+template <int MODE> Layout layout_of(int64_t rows, int64_t cols, int dtype) {
   switch (dtype) {
-    case PK_F32: return bias ? layout_for<float, true>(rows, cols) : layout_for<float, false>(rows, cols);
-    case PK_BF16: return bias ? layout_for<bf16, true>(rows, cols) : layout_for<bf16, false>(rows, cols);
-    default: return bias ? layout_for<f16, true>(rows, cols) : layout_for<f16, false>(rows, cols);
+    case PK_F32: return layout_for<float, MODE>(rows, cols);
+    case PK_BF16: return layout_for<bf16, MODE>(rows, cols);
+    default: return layout_for<f16, MODE>(rows, cols);
   }
+}
+
+Layout workspace_layout(int64_t rows, int64_t cols, int dtype, int mode) {
+  return mode == kBias ? layout_of<kBias>(rows, cols, dtype)
+                       : mode == kAdd ? layout_of<kAdd>(rows, cols, dtype) : layout_of<kPlain>(rows, cols, dtype);
+}
+
+// One workspace size serves every backward entry point and mode.
+int64_t workspace_bytes(int64_t rows, int64_t cols, int dtype) {
+  int64_t n = 0;
+  for (int mode : {kPlain, kBias, kAdd}) {
+    const int64_t t = workspace_layout(rows, cols, dtype, mode).total;
+    n = t > n ? t : n;
+  }
+  return n;
+}
+
+template <int MODE> int fwd_dispatch(const FwdArgs& a, int dtype, const char* who) {
+  switch (dtype) {
+    case PK_F32: return fwd<float, MODE>(a, who);
+    case PK_BF16: return fwd<bf16, MODE>(a, who);
+    default: return fwd<f16, MODE>(a, who);
+  }
+}
+
+template <int MODE> int bwd_dispatch(const BwdArgs& a, int dtype, const char* who) {
+  switch (dtype) {
+    case PK_F32: return bwd<float, MODE>(a, who);
+    case PK_BF16: return bwd<bf16, MODE>(a, who);
+    default: return bwd<f16, MODE>(a, who);
+  }
+}
+
+// Splits the caller's workspace for a backward call of this mode.
+int carve(const char* who, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, int mode,
+          BwdArgs& a) {
+  const Layout l = workspace_layout(rows, cols, dtype, mode);
+  if (workspace_bytes < l.total)
+    return fail(PK_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", who, (long long)workspace_bytes,
+                (long long)l.total);
+  if (!aligned16(workspace)) return fail(PK_ERR_INVALID, "%s: workspace not 16-byte aligned", who);
+  char* base = static_cast<char*>(workspace);
+  a.dw_part = reinterpret_cast<float*>(base);
+  a.db_part = mode == kBias ? reinterpret_cast<float*>(base + l.part) : nullptr;
+  a.stage = reinterpret_cast<float*>(base + l.part * (mode == kBias ? 2 : 1));
+  return PK_OK;
 }
 
 int check_shape(const char* who, int64_t rows, int64_t cols, int dtype) {
@@ -626,57 +754,61 @@ int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, floa
   if (rows == 0) return PK_OK;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_rmsnorm_fwd: zero-width rows");
   if (!x || !w || !y) return fail(PK_ERR_INVALID, "pk_rmsnorm_fwd: null pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool b = bias != nullptr;
-  switch (dtype) {
-    case PK_F32: return b ? fwd<float, true>(x, w, bias, y, rstd, rows, cols, eps, s)
-                          : fwd<float, false>(x, w, bias, y, rstd, rows, cols, eps, s);
-    case PK_BF16: return b ? fwd<bf16, true>(x, w, bias, y, rstd, rows, cols, eps, s)
-                           : fwd<bf16, false>(x, w, bias, y, rstd, rows, cols, eps, s);
-    default: return b ? fwd<f16, true>(x, w, bias, y, rstd, rows, cols, eps, s)
-                      : fwd<f16, false>(x, w, bias, y, rstd, rows, cols, eps, s);
-  }
+  const FwdArgs a{x, w, bias, nullptr, nullptr, 0.f, y, rstd, rows, (int)cols, eps, static_cast<hipStream_t>(stream)};
+  return bias != nullptr ? fwd_dispatch<kBias>(a, dtype, "pk_rmsnorm_fwd")
+                         : fwd_dispatch<kPlain>(a, dtype, "pk_rmsnorm_fwd");
 }
 
 int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype) {
   using namespace pk;
   if (rows <= 0 || cols <= 0 || !known_dtype(dtype)) return 0;
-  return workspace_layout(rows, cols, dtype, true).total;
+  return workspace_bytes(rows, cols, dtype);
 }
 
 int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
                    void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream) {
   using namespace pk;
-  if (int st = check_shape("pk_rmsnorm_bwd", rows, cols, dtype)) return st;
+  const char* who = "pk_rmsnorm_bwd";
+  if (int st = check_shape(who, rows, cols, dtype)) return st;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: zero-width rows");
   if (!x || !w || !rstd || !dy || !dx || !dw || !workspace)
     return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: null pointer");
-  const bool b = dbias != nullptr;
   if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "pk_rmsnorm_bwd: zero rows (dw is all zeros; fill it host-side)");
-  const Layout l = workspace_layout(rows, cols, dtype, b);
-  if (workspace_bytes < l.total)
-    return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
-                (long long)l.total);
-  if (!aligned16(workspace)) return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: workspace not 16-byte aligned");
-  char* base = static_cast<char*>(workspace);
-  BwdArgs a{x,
-            w,
-            dy,
-            rstd,
-            dx,
-            dw,
-            dbias,
-            reinterpret_cast<float*>(base),
-            b ? reinterpret_cast<float*>(base + l.part) : nullptr,
-            reinterpret_cast<float*>(base + l.part * (b ? 2 : 1)),
-            rows,
-            (int)cols,
+  const int mode = dbias != nullptr ? kBias : kPlain;
+  BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
-  switch (dtype) {
-    case PK_F32: return b ? bwd<float, true>(a) : bwd<float, false>(a);
-    case PK_BF16: return b ? bwd<bf16, true>(a) : bwd<bf16, false>(a);
-    default: return b ? bwd<f16, true>(a) : bwd<f16, false>(a);
-  }
+  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, mode, a)) return st;
+  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, who) : bwd_dispatch<kPlain>(a, dtype, who);
+}
+
+int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y, void* s, float* rstd,
+                       int64_t rows, int64_t cols, float eps, float offset, int dtype, void* stream) {
+  using namespace pk;
+  const char* who = "pk_add_rmsnorm_fwd";
+  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (rows == 0) return PK_OK;
+  if (cols == 0) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: zero-width rows");
+  if (!x || !residual || !w || !y || !s) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: null pointer");
+  if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: offset is not finite");
+  const FwdArgs a{x, w, nullptr, residual, s, offset, y, rstd, rows, (int)cols, eps, static_cast<hipStream_t>(stream)};
+  return fwd_dispatch<kAdd>(a, dtype, who);
+}
+
+int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const void* dy, const void* ds, void* dx,
+                       void* dw, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, float offset,
+                       int dtype, void* stream) {
+  using namespace pk;
+  const char* who = "pk_add_rmsnorm_bwd";
+  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (cols == 0) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: zero-width rows");
+  if (!s || !w || !rstd || !dy || !dx || !dw || !workspace)
+    return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: null pointer");
+  if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "pk_add_rmsnorm_bwd: zero rows (dw is all zeros; fill it host-side)");
+  if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: offset is not finite");
+  BwdArgs a{s, w, dy, ds, offset, rstd, dx, dw, nullptr, nullptr, nullptr, nullptr, rows, (int)cols,
+            static_cast<hipStream_t>(stream)};
+  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, kAdd, a)) return st;
+  return bwd_dispatch<kAdd>(a, dtype, who);
 }
 
 }  // extern "C"

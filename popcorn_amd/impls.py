@@ -8,6 +8,7 @@ reference's output structure. Arithmetic happens in the HIP kernels of
 host-side or torch fallback: an input the kernels do not cover raises.
 
     rms_norm(x, weight, bias=None, eps=1e-6)        kernels/rms_norm.py:16-30
+    add_rms_norm(x, residual, weight, eps=1e-6, offset=0.0)  kernels/add_rms_norm.py:8-26
     swiglu(a, b)                                    kernels/swiglu.py:9-18
     rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
     attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37 (forward only)
@@ -20,7 +21,7 @@ from torch import Tensor
 
 from popcorn_amd import _lib
 
-__all__ = ["rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "rotary_embedding_"]
+__all__ = ["rms_norm", "add_rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "rotary_embedding_"]
 
 
 def _require_cuda(*tensors: Tensor | None) -> torch.device:
@@ -125,6 +126,80 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
     (fp32, bf16 or fp16). Backward gives dx, dweight, dbias.
     """
     return _RMSNorm.apply(x, weight, bias, eps)
+
+
+# --------------------------------------------------------------------------- add_rms_norm
+
+
+class _AddRMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor, residual: Tensor, weight: Tensor, eps: float, offset: float):
+        device = _require_cuda(x, residual, weight)
+        dtype = _same_dtype("add_rms_norm", x, residual, weight)
+        cols = x.shape[-1]
+        if residual.shape != x.shape:
+            raise ValueError(f"popcorn_amd.add_rms_norm: residual {tuple(residual.shape)} != x {tuple(x.shape)}")
+        if weight.shape != (cols,):
+            raise ValueError(f"popcorn_amd.add_rms_norm: weight must be [{cols}]")
+        x2 = x.reshape(-1, cols).contiguous()
+        r2 = residual.reshape(-1, cols).contiguous()
+        w = weight.contiguous()
+        rows = x2.shape[0]
+        y = torch.empty_like(x2)
+        s = torch.empty_like(x2)
+        rstd = torch.empty(rows, dtype=torch.float32, device=device)
+        lib = _lib.load()
+        _lib.check(
+            lib.pk_add_rmsnorm_fwd(
+                x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
+                float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
+            ),
+            lib,
+        )
+        ctx.save_for_backward(s, w, rstd)
+        ctx.offset = float(offset)
+        ctx.shape = x.shape
+        ctx.set_materialize_grads(False)
+        return y.view(x.shape), s.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy: Tensor | None, ds: Tensor | None):
+        s, w, rstd = ctx.saved_tensors
+        rows, cols = s.shape
+        if dy is None:  # only the residual stream was used downstream
+            dsum = ds.reshape(rows, cols).to(s.dtype) if ds is not None else torch.zeros_like(s)
+            return dsum.view(ctx.shape), dsum.view(ctx.shape), torch.zeros_like(w), None, None
+        dy2 = dy.reshape(rows, cols).to(s.dtype).contiguous()
+        ds2 = ds.reshape(rows, cols).to(s.dtype).contiguous() if ds is not None else None
+        dsum = torch.empty_like(s)
+        dw = torch.empty_like(w)
+        if rows == 0:
+            dw.zero_()
+        else:
+            lib = _lib.load()
+            code = _lib.dtype_code(s.dtype)
+            nbytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, code)
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=s.device)
+            _lib.check(
+                lib.pk_add_rmsnorm_bwd(
+                    s.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(),
+                    ds2.data_ptr() if ds2 is not None else None, dsum.data_ptr(), dw.data_ptr(),
+                    workspace.data_ptr(), nbytes, rows, cols, ctx.offset, code, _lib.stream_handle(s.device),
+                ),
+                lib,
+            )
+        # s = x + residual: both receive the gradient of s (as torch's add backward hands them)
+        return dsum.view(ctx.shape), dsum.view(ctx.shape), dw, None, None
+
+
+def add_rms_norm(x: Tensor, residual: Tensor, weight: Tensor, eps: float = 1e-6,
+                 offset: float = 0.0) -> tuple[Tensor, Tensor]:
+    """(y, s): s = round(x + residual), y = round(round(s * rsqrt(mean(s^2) + eps)) * round(weight + offset)).
+
+    x, residual [..., hidden]; weight [hidden]; one dtype for all. Backward gives
+    d(x) = d(residual) and dweight.
+    """
+    return _AddRMSNorm.apply(x, residual, weight, eps, offset)
 
 
 # --------------------------------------------------------------------------- swiglu

@@ -74,6 +74,16 @@ def test_rms_norm_records_and_routes_with_grad():
     _check_record_and_route(op, record, lambda: op(x, w))
 
 
+def test_add_rms_norm_records_and_routes_with_grad():
+    """Two outputs (y, s), both graded with their own cotangents, and offset 1.0 from the test pool."""
+    op = compat.KERNELS["add_rms_norm"]
+    x, res = _randn(4096, 4096).requires_grad_(), _randn(4096, 4096, seed=2).requires_grad_()
+    w = (1 + 0.1 * _randn(4096, dtype=torch.float32, seed=1)).bfloat16().requires_grad_()
+    [record] = op.benchmark(x, res, w, 1e-6, 1.0, backend=NAME)
+    assert record.result.grad and {"x", "residual", "weight"} <= set(record.result.bwd)
+    _check_record_and_route(op, record, lambda: op(x, res, w, 1e-6, 1.0))
+
+
 def test_swiglu_records_and_routes_with_grad():
     op = compat.KERNELS["swiglu"]
     a, b = _randn(4096, 8192).requires_grad_(), _randn(4096, 8192, seed=1).requires_grad_()

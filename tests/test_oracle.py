@@ -104,6 +104,70 @@ def test_rms_norm_bwd_orthogonal_to_x():
     np.testing.assert_allclose(np.sum(dx * x, axis=-1), 0.0, atol=1e-12)
 
 
+# --------------------------------------------------------------------------- add_rms_norm
+
+
+def test_add_rms_norm_matches_torch_functional():
+    r = rng(41)
+    x, res = r.standard_normal((3, 5, 40)), r.standard_normal((3, 5, 40))
+    w = 1 + 0.1 * r.standard_normal(40)
+    for eps, offset in ((1e-6, 0.0), (1e-5, 1.0), (0.2, -0.5)):
+        y, s = O.add_rms_norm(x, res, w, eps, offset)
+        st = torch.from_numpy(x) + torch.from_numpy(res)
+        want = F.rms_norm(st, (40,), torch.from_numpy(w) + offset, eps=eps).numpy()
+        np.testing.assert_allclose(y, want, rtol=1e-13, atol=1e-13)
+        np.testing.assert_array_equal(s, x + res)
+
+
+def test_add_rms_norm_reduces_to_rms_norm():
+    r = rng(42)
+    x, w = r.standard_normal((6, 24)), r.standard_normal(24)
+    y, s = O.add_rms_norm(x, np.zeros_like(x), w, 1e-6, 0.0)
+    np.testing.assert_array_equal(y, O.rms_norm(x, w, None, 1e-6))
+    np.testing.assert_array_equal(s, x)
+
+
+def test_add_rms_norm_bwd_matches_torch_autograd_through_both_outputs():
+    r = rng(43)
+    x, res, dy, ds = (r.standard_normal((4, 2, 32)) for _ in range(4))
+    w = 1 + 0.1 * r.standard_normal(32)
+    for offset, with_ds in ((0.0, True), (1.0, True), (1.0, False)):
+        xt, rt, wt = (torch.from_numpy(a).requires_grad_() for a in (x, res, w))
+        st = xt + rt
+        yt = F.rms_norm(st, (32,), wt + offset, eps=1e-5)
+        loss = (yt * torch.from_numpy(dy)).sum() + ((st * torch.from_numpy(ds)).sum() if with_ds else 0.0)
+        gx, gr, gw = torch.autograd.grad(loss, (xt, rt, wt))
+        dx, dres, dw = O.add_rms_norm_bwd(x, res, w, dy, ds if with_ds else None, 1e-5, offset)
+        np.testing.assert_allclose(dx, gx.numpy(), rtol=1e-11, atol=1e-12)
+        np.testing.assert_allclose(dres, gr.numpy(), rtol=1e-11, atol=1e-12)
+        np.testing.assert_allclose(dw, gw.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_add_rms_norm_bwd_finite_differences():
+    r = rng(44)
+    x, res, dy, ds = (r.standard_normal((2, 7)) for _ in range(4))
+    w = r.standard_normal(7)
+    eps, offset, h = 1e-3, 0.75, 1e-6
+
+    def loss(xv, rv, wv):
+        y, s = O.add_rms_norm(xv, rv, wv, eps, offset)
+        return float(np.sum(y * dy) + np.sum(s * ds))
+
+    dx, dres, dw = O.add_rms_norm_bwd(x, res, w, dy, ds, eps, offset)
+    for grad, which in ((dx, 0), (dres, 1), (dw, 2)):
+        args = [x, res, w]
+        base = args[which]
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            plus, minus = base.copy(), base.copy()
+            plus[idx] += h
+            minus[idx] -= h
+            a_p, a_m = list(args), list(args)
+            a_p[which], a_m[which] = plus, minus
+            num[idx] = (loss(*a_p) - loss(*a_m)) / (2 * h)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-7)
+
+
 # --------------------------------------------------------------------------- swiglu
 
 
@@ -306,3 +370,15 @@ def test_planted_mistakes_are_caught(monkeypatch):
     da_bad = g * b * sg
     da, _ = O.swiglu_bwd(g, a, b)
     assert not np.allclose(da, da_bad)
+
+    # add_rms_norm backward that forgets the offset, or drops the gradient reaching s directly
+    xa, ra, dya, dsa = (r.standard_normal((2, 12)) for _ in range(4))
+    wa = 1 + 0.1 * r.standard_normal(12)
+    xt, rt, wt = (torch.from_numpy(v).requires_grad_() for v in (xa, ra, wa))
+    st = xt + rt
+    loss = (F.rms_norm(st, (12,), wt + 1.0, eps=1e-6) * torch.from_numpy(dya)).sum() + (st * torch.from_numpy(dsa)).sum()
+    gx, _, _ = torch.autograd.grad(loss, (xt, rt, wt))
+    no_offset, _, _ = O.add_rms_norm_bwd(xa, ra, wa, dya, dsa, 1e-6, 0.0)
+    no_ds, _, _ = O.add_rms_norm_bwd(xa, ra, wa, dya, None, 1e-6, 1.0)
+    assert not np.allclose(no_offset, gx.numpy())
+    assert not np.allclose(no_ds, gx.numpy())
