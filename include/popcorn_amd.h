@@ -136,6 +136,23 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
                 int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
                 int causal, int dtype, void* stream);
 
+/*
+ * Attention forward over packed variable-length sequences: sequence i is
+ * tokens [cu_seqlens[i], cu_seqlens[i+1]) of q [total, q_heads, head_dim] and
+ * k, v [total, kv_heads, head_dim], attended independently (causal masks are
+ * top-left aligned within each sequence); o is like q. cu_seqlens is an int32
+ * device array of num_seqs + 1 non-decreasing offsets from 0 to total, and
+ * max_seqlen is at least its largest difference (values are clamped to
+ * [0, total] on the device). lse (fp32 [q_heads, total], natural log) may be
+ * NULL. strides[8] = q, k, v, o (token, head) strides in elements. Same dtypes
+ * and head_dim as pk_attn_fwd.
+ * Replaces: reference `attn_varlen` (kernels/attn_varlen.py:15-54, SDPA per
+ * cu_seqlens segment).
+ */
+int pk_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int* cu_seqlens,
+                       const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

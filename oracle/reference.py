@@ -28,6 +28,9 @@ independent fact that a plausible slip would break:
                     norm preservation for unit tables; conjugate inverts forward
   attention         explicit per-query loops; float64 SDPA with repeat_interleave;
                     q = 0 gives prefix means of v and lse = log(t + 1); S = 1 gives v
+  attention_varlen  one segment equals `attention`; segments are independent
+                    (changing one leaves the others' rows bit-identical);
+                    length-1 segments give v
 No function here is "parity unpinned".
 """
 
@@ -46,6 +49,7 @@ __all__ = [
     "rotary_embedding_bwd",
     "attention",
     "attention_rows",
+    "attention_varlen",
 ]
 
 
@@ -210,4 +214,23 @@ def attention(q, k, v, causal: bool = False, scale: float | None = None):
             total = p.sum(axis=-1, keepdims=True)
             o[b, :, h] = p @ vh / total
             lse[b, h] = (m + np.log(total))[:, 0]
+    return o, lse
+
+
+def attention_varlen(q, k, v, cu_seqlens, causal: bool = False, scale: float | None = None):
+    """Packed-sequence attention: q [total, Hq, D], k, v [total, Hkv, D], segments
+    [cu[i], cu[i+1]) attended independently (kernels/attn_varlen.py:41-54).
+
+    Returns (o [total, Hq, D], lse [Hq, total]).
+    """
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    bounds = [int(c) for c in np.asarray(cu_seqlens).tolist()]
+    o = np.empty_like(q)
+    lse = np.empty((q.shape[1], q.shape[0]))
+    for lo, hi in zip(bounds, bounds[1:]):
+        if hi == lo:
+            continue
+        oo, ll = attention(q[None, lo:hi], k[None, lo:hi], v[None, lo:hi], causal, scale)
+        o[lo:hi] = oo[0]
+        lse[:, lo:hi] = ll[0]
     return o, lse

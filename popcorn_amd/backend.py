@@ -94,6 +94,21 @@ def attn_supported(q, k, v, causal, softmax_scale) -> bool:
     )
 
 
+def attn_varlen_supported(q, k, v, cu_seqlens, causal, softmax_scale) -> bool:
+    return (
+        _on_hip(q, k, v)
+        and isinstance(cu_seqlens, torch.Tensor)
+        and not cu_seqlens.is_floating_point()
+        and cu_seqlens.dim() == 1
+        and q.dtype in (torch.bfloat16, torch.float16)
+        and q.dtype == k.dtype == v.dtype
+        and q.dim() == 3
+        and q.shape[-1] in (64, 128)
+        and k.shape[1] > 0
+        and q.shape[1] % k.shape[1] == 0
+    )
+
+
 # (op, source, predicate, forward_only): attention has no backward kernel yet,
 # so Popcorn declines it whenever a call needs gradients.
 REGISTRATIONS = (
@@ -102,6 +117,7 @@ REGISTRATIONS = (
     ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
     ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
     ("attn", "popcorn_amd.impls.attn", attn_supported, True),
+    ("attn_varlen", "popcorn_amd.impls.attn_varlen", attn_varlen_supported, True),
 )
 
 

@@ -14,7 +14,7 @@ from popcorn_amd.compat.errors import BackendUnavailableError, BackendVersionErr
 from popcorn_amd.compat.harness import compare_inputs, report
 from popcorn_amd.compat.records import Case, Record
 from popcorn_amd.compat.selection import Range
-from popcorn_amd.compat.shapes import BFloat16, Float, Float16, Float32, Float64
+from popcorn_amd.compat.shapes import BFloat16, Float, Float16, Float32, Float64, Int32
 from popcorn_amd.compat.sources import declare_backend, kernel
 from popcorn_amd.compat import harness, store  # noqa: E402
 from popcorn_amd.compat import kernels  # noqa: E402  registers the four ops
@@ -22,5 +22,5 @@ from popcorn_amd.compat import kernels  # noqa: E402  registers the four ops
 __all__ = [
     "KERNELS", "Dispatcher", "Implementation", "register_kernel", "BackendUnavailableError", "BackendVersionError",
     "DispatchError", "PopcornError", "compare_inputs", "report", "Case", "Record", "Range", "BFloat16", "Float",
-    "Float16", "Float32", "Float64", "declare_backend", "kernel", "kernels", "harness", "store",
+    "Float16", "Float32", "Float64", "Int32", "declare_backend", "kernel", "kernels", "harness", "store",
 ]

@@ -2,7 +2,8 @@
 
 Signatures, shape annotations and test-argument pools are Popcorn's
 (kernels/rms_norm.py:16-30, kernels/add_rms_norm.py:8-26, kernels/swiglu.py:9-18,
-kernels/rotary_embedding.py:12-40, kernels/attn.py:10-37); the arithmetic is
+kernels/rotary_embedding.py:12-40, kernels/attn.py:10-37,
+kernels/attn_varlen.py:15-54); the arithmetic is
 the eager-torch restatement in `popcorn_amd.compat.references`.
 """
 
@@ -10,7 +11,7 @@ from torch import Tensor
 
 from popcorn_amd.compat import references
 from popcorn_amd.compat.dispatcher import register_kernel
-from popcorn_amd.compat.shapes import Float
+from popcorn_amd.compat.shapes import Float, Int32
 
 
 @register_kernel(test_args={"eps": [1e-6, 1e-5]})
@@ -63,3 +64,16 @@ def attn(
 ) -> Float[Tensor, "batch seq q_heads head_dim"]:
     """Multi-head attention with grouped kv heads (q_heads a multiple of kv_heads)."""
     return references.attn(q, k, v, causal, softmax_scale)
+
+
+@register_kernel(test_args={"softmax_scale": [None, 0.25]}, test_inputs={"cu_seqlens": references.cuts})
+def attn_varlen(
+    q: Float[Tensor, "total q_heads head_dim"],
+    k: Float[Tensor, "total kv_heads head_dim"],
+    v: Float[Tensor, "total kv_heads head_dim"],
+    cu_seqlens: Int32[Tensor, "boundaries"],
+    causal: bool = False,
+    softmax_scale: float | None = None,
+) -> Float[Tensor, "total q_heads head_dim"]:
+    """Attention over packed variable-length sequences, each attended independently."""
+    return references.attn_varlen(q, k, v, cu_seqlens, causal, softmax_scale)

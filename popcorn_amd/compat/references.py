@@ -11,6 +11,7 @@ the native-dtype rounding the budget measures:
     swiglu            kernels/swiglu.py:9-18
     rotary_embedding  kernels/rotary_embedding.py:12-40
     attn              kernels/attn.py:10-37
+    attn_varlen       kernels/attn_varlen.py:15-54 (`cuts`: kernels/_varlen.py:8-13)
 """
 
 from __future__ import annotations
@@ -100,3 +101,27 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
         scores = scores.masked_fill(mask, float("-inf"))
     out = torch.matmul(torch.softmax(scores, dim=-1), vh)
     return out.transpose(1, 2)
+
+
+def attn_varlen(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, causal: bool = False,
+                softmax_scale: float | None = None) -> Tensor:
+    """`attn` on each packed segment [cu[i], cu[i+1]) of [total, heads, dim] tensors, concatenated."""
+    bounds = cu_seqlens.tolist()
+    return torch.cat([
+        attn(q[lo:hi][None], k[lo:hi][None], v[lo:hi][None], causal, softmax_scale)[0]
+        for lo, hi in zip(bounds, bounds[1:])
+    ])
+
+
+def cuts(t: Tensor, dims, generator: torch.Generator) -> Tensor:
+    """Random cu_seqlens for `total` tokens: len(t) - 1 non-empty segments, offsets from 0 to total.
+
+    Popcorn's test-input transform for packed sequences (kernels/_varlen.py:8-13):
+    the inner offsets are the first segments - 1 entries of a seeded random
+    permutation of 1 .. total - 1, sorted.
+    """
+    total, segments = dims["total"], t.shape[-1] - 1
+    if total < segments:
+        raise ValueError(f"total={total} cannot hold {segments} non-empty segments")
+    inner = (torch.randperm(total - 1, generator=generator)[: segments - 1] + 1).sort().values
+    return torch.cat([torch.zeros(1, dtype=inner.dtype), inner, torch.full((1,), total, dtype=inner.dtype)]).int()

@@ -76,6 +76,7 @@ Float16 = _Family("Float16", ("float16",))
 BFloat16 = _Family("BFloat16", ("bfloat16",))
 Float32 = _Family("Float32", ("float32",))
 Float64 = _Family("Float64", ("float64",))
+Int32 = _Family("Int32", ("int32",))
 
 Token = typing.Union[str, int, "types.EllipsisType"]
 

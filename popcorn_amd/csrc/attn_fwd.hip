@@ -96,11 +96,15 @@ struct AttnArgs {
   const void* v;
   void* o;
   float* lse;
+  // Packed sequences: sequence b holds tokens [cu[b], cu[b+1]) of `total`,
+  // batch strides are 0 and S is the longest sequence. NULL: a dense batch.
+  const int* cu;
+  int total;
   int64_t qsb, qss, qsh, ksb, kss, ksh, vsb, vss, vsh, osb, oss, osh;
+  int64_t lse_bs, lse_hs;  // lse element (b, h, token t of b) at b*lse_bs + h*lse_hs + t (+ cu[b] when packed)
   int B, S, Hq, Hkv, group, m_tiles;
-  int k_bytes, v_bytes;  // bytes from a (batch, kv head) base to the end of its last row
-  float c;               // |scale| * log2(e), at least 1e-30
-  uint32_t q_flip;       // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
+  float c;          // |scale| * log2(e), at least 1e-30
+  uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
 
 __device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
@@ -143,31 +147,40 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int hkv = rest % a.Hkv;
   const int hq = hkv * G + hig;
 
+  // this block's sequence: all of it for a dense batch; tokens [cu[b], cu[b+1])
+  // of a packed one (clamped, so a malformed table cannot address past `total`)
+  int S = a.S, start = 0;
+  if (a.cu != nullptr) {
+    start = min(max(a.cu[b], 0), a.total);
+    S = min(min(max(a.cu[b + 1], start), a.total) - start, a.S);
+  }
+  const int m0 = m_tile * BM;
+  if (m0 >= S) return;  // whole block: before any barrier
+
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r32 = lane & 31;
   const int g = lane >> 5;
-  const int m0 = m_tile * BM;
   const int wave_first = m0 + wave * 32;
   const int q_row = wave_first + r32;
 
-  const T* qbase = static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh;
-  const T* kbase = static_cast<const T*>(a.k) + b * a.ksb + hkv * a.ksh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.vsb + hkv * a.vsh;
-  // K/V of this (batch, kv head) through buffer resources: rows at or past S
-  // read as zero (range-checked), and a tile's base is one scalar offset.
-  const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, a.k_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, a.v_bytes, 0x00020000);
+  const T* qbase = static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh + start * a.qss;
+  const T* kbase = static_cast<const T*>(a.k) + b * a.ksb + hkv * a.ksh + start * a.kss;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.vsb + hkv * a.vsh + start * a.vss;
+  // K/V of this (sequence, kv head) through buffer resources: rows at or past
+  // S read as zero (range-checked), and a tile's base is one scalar offset.
+  const int k_bytes = (int)(((int64_t)(S - 1) * a.kss + D) * (int)sizeof(T));
+  const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + D) * (int)sizeof(T));
+  const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
   Frag qf[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
     uint4 raw = make_uint4(0, 0, 0, 0);
-    if (q_row < a.S) raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
+    if (q_row < S) raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
     raw.x ^= a.q_flip;
     raw.y ^= a.q_flip;
     raw.z ^= a.q_flip;
@@ -175,7 +188,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     qf[kk] = __builtin_bit_cast(Frag, raw);
   }
 
-  const int kv_end = CAUSAL ? min(m0 + BM, a.S) : a.S;
+  const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
   // ---- tile staging: K rows by 16-byte chunk, V rows V_RPT at a time
@@ -218,10 +231,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     return s;
   };
   // whether tile t holds keys some row of this wave must not see
-  auto need_mask = [&](int t) { return (CAUSAL && t * BN + BN - 1 > wave_first) || t * BN + BN > a.S; };
+  auto need_mask = [&](int t) { return (CAUSAL && t * BN + BN - 1 > wave_first) || t * BN + BN > S; };
   auto apply_mask = [&](int t, f32x16& s) {
     // last visible key of this lane's query; rows past the end (zero loads) are masked too
-    const int lim = CAUSAL ? min(q_row, a.S - 1) : a.S - 1;
+    const int lim = CAUSAL ? min(q_row, S - 1) : S - 1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = t * BN + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -354,8 +367,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // ---- epilogue
   const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  if (q_row < a.S) {
-    T* orow = static_cast<T*>(a.o) + b * a.osb + hq * a.osh + (int64_t)q_row * a.oss;
+  if (q_row < S) {
+    T* orow = static_cast<T*>(a.o) + b * a.osb + hq * a.osh + (int64_t)(start + q_row) * a.oss;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -368,7 +381,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         *reinterpret_cast<uint2*>(orow + d0) = make_uint2(lo, hi);
       }
     if (a.lse != nullptr && g == 0)
-      a.lse[((int64_t)b * a.Hq + hq) * a.S + q_row] = (m_i + log2f(l_tot)) * 0.69314718055994530942f;
+      a.lse[b * a.lse_bs + hq * a.lse_hs + start + q_row] = (m_i + log2f(l_tot)) * 0.69314718055994530942f;
   }
 }
 
@@ -385,38 +398,32 @@ int launch(const AttnArgs& a, bool causal, hipStream_t s) {
 }  // namespace
 }  // namespace pk
 
-extern "C" {
+namespace pk {
+namespace {
 
-int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int64_t* strides,
-                int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
-                int causal, int dtype, void* stream) {
-  using namespace pk;
+// Checks shared by the dense and the packed entry point, then the launch.
+// strides: q, k, v, o (batch, token, head) in elements; `seq` is the longest
+// sequence, `batch` the number of sequences.
+int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t batch, int64_t seq, int64_t q_heads,
+                int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
   if (batch < 0 || seq < 0 || q_heads < 0 || kv_heads < 0 || head_dim < 0)
-    return fail(PK_ERR_INVALID, "pk_attn_fwd: negative size");
+    return fail(PK_ERR_INVALID, "%s: negative size", who);
   if (batch == 0 || seq == 0 || q_heads == 0) return PK_OK;
-  if (!q || !k || !v || !o || !strides) return fail(PK_ERR_INVALID, "pk_attn_fwd: null pointer");
+  if (!a.q || !a.k || !a.v || !a.o || !strides) return fail(PK_ERR_INVALID, "%s: null pointer", who);
   if (kv_heads == 0 || q_heads % kv_heads != 0)
-    return fail(PK_ERR_INVALID, "pk_attn_fwd: q_heads=%lld is not a multiple of kv_heads=%lld", (long long)q_heads,
+    return fail(PK_ERR_INVALID, "%s: q_heads=%lld is not a multiple of kv_heads=%lld", who, (long long)q_heads,
                 (long long)kv_heads);
-  if (dtype != PK_BF16 && dtype != PK_F16)
-    return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: dtype code %d (bf16/fp16 only)", dtype);
+  if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
   if (head_dim != 64 && head_dim != 128)
-    return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: head_dim=%lld (64 or 128 only)", (long long)head_dim);
-  if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "pk_attn_fwd: softmax_scale is not finite");
-  if (seq > (1 << 30) || batch * q_heads > (1 << 20))
-    return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: shape too large");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
-    return fail(PK_ERR_INVALID, "pk_attn_fwd: q/k/v/o must be 16-byte aligned");
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (64 or 128 only)", who, (long long)head_dim);
+  if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
+  if (seq > (1 << 30) || batch * q_heads > (1 << 20)) return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
+  if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.o))
+    return fail(PK_ERR_INVALID, "%s: q/k/v/o must be 16-byte aligned", who);
   for (int i = 0; i < 12; ++i)
     if (strides[i] % 8 != 0 || strides[i] < 0)
-      return fail(PK_ERR_INVALID, "pk_attn_fwd: stride %d = %lld is not a non-negative multiple of 8", i,
+      return fail(PK_ERR_INVALID, "%s: stride %d = %lld is not a non-negative multiple of 8", who, i,
                   (long long)strides[i]);
-  AttnArgs a{};
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.o = o;
-  a.lse = lse;
   a.qsb = strides[0];
   a.qss = strides[1];
   a.qsh = strides[2];
@@ -435,20 +442,66 @@ int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse
   a.Hkv = (int)kv_heads;
   a.group = (int)(q_heads / kv_heads);
   a.m_tiles = (int)((seq + BM - 1) / BM);
-  // Buffer offsets are 32-bit: the tile loads reach up to two tiles past the
-  // last one (reading zeros there), and every such offset must fit.
-  const int64_t k_span = ((seq - 1) * strides[4] + head_dim) * 2, v_span = ((seq - 1) * strides[7] + head_dim) * 2;
+  // Buffer offsets are 32-bit: within one sequence the tile loads reach up to
+  // two tiles past its last row (reading zeros there), and every such offset
+  // must fit.
   const int64_t reach = (seq + 3 * BN) * (strides[4] > strides[7] ? strides[4] : strides[7]) * 2 + head_dim * 2;
-  if (reach > INT32_MAX)
-    return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: K/V rows span more than 2 GiB per head");
-  a.k_bytes = (int)k_span;
-  a.v_bytes = (int)v_span;
+  if (reach > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: K/V rows span more than 2 GiB per head", who);
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
-  if ((int64_t)a.m_tiles * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "pk_attn_fwd: grid too large");
+  if ((int64_t)a.m_tiles * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PK_BF16) return head_dim == 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
   return head_dim == 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
+}
+
+}  // namespace
+}  // namespace pk
+
+extern "C" {
+
+int pk_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int64_t* strides,
+                int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
+                int causal, int dtype, void* stream) {
+  using namespace pk;
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.cu = nullptr;
+  a.lse_bs = q_heads * seq;  // [batch, q_heads, seq]
+  a.lse_hs = seq;
+  return attn_launch("pk_attn_fwd", a, strides, batch, seq, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
+                     stream);
+}
+
+int pk_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, float* lse, const int* cu_seqlens,
+                       const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
+  using namespace pk;
+  const char* who = "pk_attn_varlen_fwd";
+  if (num_seqs < 0 || total < 0 || max_seqlen < 0) return fail(PK_ERR_INVALID, "%s: negative size", who);
+  if (num_seqs == 0 || total == 0 || max_seqlen == 0) return PK_OK;
+  if (!cu_seqlens || !strides) return fail(PK_ERR_INVALID, "%s: null pointer", who);
+  if (total > INT32_MAX || max_seqlen > total) return fail(PK_ERR_INVALID, "%s: max_seqlen %lld exceeds total %lld", who,
+                                                        (long long)max_seqlen, (long long)total);
+  // packed tensors have no batch dimension: strides are (token, head) of q, k, v, o
+  const int64_t dense[12] = {0, strides[0], strides[1], 0, strides[2], strides[3],
+                             0, strides[4], strides[5], 0, strides[6], strides[7]};
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.cu = cu_seqlens;
+  a.total = (int)total;
+  a.lse_bs = 0;  // [q_heads, total]
+  a.lse_hs = total;
+  return attn_launch(who, a, dense, num_seqs, max_seqlen, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
+                     stream);
 }
 
 }  // extern "C"

@@ -12,6 +12,8 @@ host-side or torch fallback: an input the kernels do not cover raises.
     swiglu(a, b)                                    kernels/swiglu.py:9-18
     rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
     attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37 (forward only)
+    attn_varlen(q, k, v, cu_seqlens, causal=False, softmax_scale=None)
+                                                    kernels/attn_varlen.py:15-54 (forward only)
 """
 
 from __future__ import annotations
@@ -21,7 +23,8 @@ from torch import Tensor
 
 from popcorn_amd import _lib
 
-__all__ = ["rms_norm", "add_rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "rotary_embedding_"]
+__all__ = ["rms_norm", "add_rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "attn_varlen",
+           "attn_varlen_with_lse", "rotary_embedding_"]
 
 
 def _require_cuda(*tensors: Tensor | None) -> torch.device:
@@ -389,5 +392,65 @@ def _attention(q, k, v, causal, softmax_scale, want_lse):
 
 def _aligned_rows(t: Tensor) -> Tensor:
     """A view the kernel can read with 16-byte loads, copying only when it must."""
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 and s >= 0 for s in t.stride()[:3])
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 and s >= 0 for s in t.stride()[:-1])
     return t if ok else t.contiguous()
+
+
+def attn_varlen_with_lse(
+    q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, causal: bool = False, softmax_scale: float | None = None
+) -> tuple[Tensor, Tensor]:
+    """Packed-sequence attention returning (o [total, q_heads, head_dim], lse [q_heads, total] fp32)."""
+    return _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse=True)
+
+
+def attn_varlen(
+    q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, causal: bool = False, softmax_scale: float | None = None
+) -> Tensor:
+    """Attention over packed variable-length sequences, each attended independently; forward only.
+
+    q [total, q_heads, head_dim], k, v [total, kv_heads, head_dim]; cu_seqlens
+    int32 [num_seqs + 1] offsets from 0 to total (the flash-attention varlen
+    layout). Causal masks are top-left aligned within each sequence.
+    """
+    return _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse=False)[0]
+
+
+def _cut_points(cu_seqlens: Tensor, total: int) -> tuple[Tensor, int, int]:
+    """(cu_seqlens as an int32 device tensor, number of sequences, longest sequence); one host read."""
+    if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2 or cu_seqlens.is_floating_point():
+        raise ValueError("popcorn_amd.attn_varlen: cu_seqlens must be a 1-D integer tensor of num_seqs + 1 offsets")
+    cuts = cu_seqlens.tolist()
+    if cuts[0] != 0 or cuts[-1] != total or any(b < a for a, b in zip(cuts, cuts[1:])):
+        raise ValueError(f"popcorn_amd.attn_varlen: cu_seqlens must rise from 0 to total={total}, got {cuts[:8]}...")
+    longest = max(b - a for a, b in zip(cuts, cuts[1:]))
+    return cu_seqlens, len(cuts) - 1, longest
+
+
+def _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse):
+    device = _require_cuda(q, k, v)
+    dtype = _same_dtype("attn_varlen", q, k, v)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise RuntimeError("popcorn_amd.attn_varlen is forward-only; call it under torch.no_grad() or on detached inputs")
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape:
+        raise ValueError("popcorn_amd.attn_varlen: q [total, hq, d] and k, v [total, hkv, d] expected")
+    total, q_heads, head_dim = q.shape
+    if k.shape[0] != total or k.shape[2] != head_dim:
+        raise ValueError(f"popcorn_amd.attn_varlen: k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    cu, num_seqs, longest = _cut_points(cu_seqlens, total)
+    cu = cu.to(device=device, dtype=torch.int32).contiguous()
+    kv_heads = k.shape[1]
+    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+    q_, k_, v_ = (_aligned_rows(t) for t in (q, k, v))
+    o = torch.empty((total, q_heads, head_dim), dtype=dtype, device=device)
+    lse = torch.empty((q_heads, total), dtype=torch.float32, device=device) if want_lse else None
+    lib = _lib.load()
+    strides = (_lib._i64 * 8)(*(s for t in (q_, k_, v_, o) for s in t.stride()[:2]))
+    _lib.check(
+        lib.pk_attn_varlen_fwd(
+            q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
+            cu.data_ptr(), strides, num_seqs, total, longest, q_heads, kv_heads, head_dim, scale, int(bool(causal)),
+            _lib.dtype_code(dtype), _lib.stream_handle(device),
+        ),
+        lib,
+    )
+    return o, lse

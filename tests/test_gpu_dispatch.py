@@ -113,6 +113,17 @@ def test_attn_forward_only_records_and_routes():
     assert _selected(op) == "torch"
 
 
+def test_attn_varlen_forward_only_records_and_routes():
+    op = compat.KERNELS["attn_varlen"]
+    total = 3000
+    q, k, v = _randn(total, 8, 128), _randn(total, 2, 128, seed=1), _randn(total, 2, 128, seed=2)
+    cu = torch.tensor([0, 1000, 1001, 2500, total], dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        [record] = op.benchmark(q, k, v, cu, True, backend=NAME)
+        assert not record.result.grad
+        _check_record_and_route(op, record, lambda: op(q, k, v, cu, True))
+
+
 def test_mixed_dtype_rotary_is_served_in_registration_order():
     """bf16 x with fp32 tables has no single dtype, so no record applies (core/config.py:95-99)."""
     op = compat.KERNELS["rotary_embedding"]

@@ -326,6 +326,41 @@ def test_attention_gqa_head_map():
     np.testing.assert_allclose(o[:, :, 1:2], o1, rtol=1e-13)
 
 
+# --------------------------------------------------------------------------- attention_varlen
+
+
+def test_attention_varlen_single_segment_is_dense_attention():
+    r = rng(51)
+    q, k, v = r.standard_normal((13, 4, 8)), r.standard_normal((13, 2, 8)), r.standard_normal((13, 2, 8))
+    for causal in (False, True):
+        o, lse = O.attention_varlen(q, k, v, [0, 13], causal, 0.4)
+        od, ld = O.attention(q[None], k[None], v[None], causal, 0.4)
+        np.testing.assert_array_equal(o, od[0])
+        np.testing.assert_array_equal(lse, ld[0])
+
+
+def test_attention_varlen_segments_are_independent():
+    r = rng(52)
+    q, k, v = r.standard_normal((20, 4, 8)), r.standard_normal((20, 1, 8)), r.standard_normal((20, 1, 8))
+    cu = [0, 7, 8, 20]
+    o, lse = O.attention_varlen(q, k, v, cu, True)
+    k2, v2 = k.copy(), v.copy()
+    k2[8:] += 5.0
+    v2[8:] -= 3.0
+    o2, lse2 = O.attention_varlen(q, k2, v2, cu, True)
+    np.testing.assert_array_equal(o[:8], o2[:8])  # the first two segments never see the third
+    np.testing.assert_array_equal(lse[:, :8], lse2[:, :8])
+    assert not np.allclose(o[8:], o2[8:])
+    np.testing.assert_allclose(o[7], np.repeat(v[7], 4, axis=0), rtol=1e-15)  # length-1 segment: o = v
+    # matches float64 SDPA run per segment
+    for lo, hi in zip(cu, cu[1:]):
+        qt = torch.from_numpy(q[lo:hi]).transpose(0, 1)
+        kt = torch.from_numpy(k[lo:hi]).repeat_interleave(4, 1).transpose(0, 1)
+        vt = torch.from_numpy(v[lo:hi]).repeat_interleave(4, 1).transpose(0, 1)
+        want = F.scaled_dot_product_attention(qt, kt, vt, is_causal=True).transpose(0, 1).numpy()
+        np.testing.assert_allclose(o[lo:hi], want, rtol=1e-12, atol=1e-12)
+
+
 # --------------------------------------------------------------------------- planted mistakes
 
 
