@@ -153,6 +153,33 @@ int pk_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, flo
                        const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
                        int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
 
+/*
+ * Attention backward for pk_attn_fwd: given o, the upstream gradient dout
+ * (like o) and the forward's lse, writes dq (like q), dk and dv (like k, v).
+ * dsum is caller scratch shaped like lse (fp32 [batch, q_heads, seq]); it
+ * receives D = rowsum(dout * o). Arithmetic: P is recomputed from q, k and
+ * lse; dS = P (dP - D); dq = scale dS k, dk = scale dS^T q (summed over the q
+ * heads of each kv head), dv = P^T dout; fp32 accumulation, one rounding per
+ * output, no atomics (the result is deterministic). strides[24] = q, k, v, o,
+ * dout, dq, dk, dv (batch, token, head) strides in elements.
+ * Replaces torch autograd of the reference `attn` (kernels/attn.py:30-37).
+ */
+int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                float* dsum, void* dq, void* dk, void* dv, const int64_t* strides, int64_t batch, int64_t seq,
+                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype,
+                void* stream);
+
+/*
+ * Backward of pk_attn_varlen_fwd (packed sequences). lse and dsum are fp32
+ * [q_heads, total]; strides[16] = q, k, v, o, dout, dq, dk, dv (token, head).
+ * Replaces torch autograd of the reference `attn_varlen`
+ * (kernels/attn_varlen.py:41-54).
+ */
+int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                       float* dsum, void* dq, void* dk, void* dv, const int* cu_seqlens, const int64_t* strides,
+                       int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads, int64_t kv_heads,
+                       int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

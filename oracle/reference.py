@@ -28,6 +28,9 @@ independent fact that a plausible slip would break:
                     norm preservation for unit tables; conjugate inverts forward
   attention         explicit per-query loops; float64 SDPA with repeat_interleave;
                     q = 0 gives prefix means of v and lse = log(t + 1); S = 1 gives v
+  attention_bwd     float64 torch autograd of SDPA (repeat_interleave grouping);
+                    central finite differences; a scale of 0 gives dq = dk = 0
+  attention_varlen_bwd  segments are independent; one segment equals attention_bwd
   attention_varlen  one segment equals `attention`; segments are independent
                     (changing one leaves the others' rows bit-identical);
                     length-1 segments give v
@@ -50,6 +53,8 @@ __all__ = [
     "attention",
     "attention_rows",
     "attention_varlen",
+    "attention_bwd",
+    "attention_varlen_bwd",
 ]
 
 
@@ -234,3 +239,50 @@ def attention_varlen(q, k, v, cu_seqlens, causal: bool = False, scale: float | N
         o[lo:hi] = oo[0]
         lse[:, lo:hi] = ll[0]
     return o, lse
+
+
+def attention_bwd(q, k, v, do, causal: bool = False, scale: float | None = None):
+    """Gradients of `attention` for cotangent do: (dq, dk, dv), shapes of q, k, v.
+
+    Per (batch, q head) with z = scale q k^T (+ mask), P = softmax(z), o = P v:
+      dv += P^T do,  dP = do v^T,  dz = P (dP - rowsum(do * o)),
+      dq = scale dz k,  dk += scale dz^T q,
+    where dk and dv of a kv head sum over the q heads that read it (h // group).
+    """
+    q, k, v, g = _f64(q), _f64(k), _f64(v), _f64(do)
+    batch, seq, hq, d = q.shape
+    hkv = k.shape[2]
+    group = hq // hkv
+    scale = d**-0.5 if scale is None else scale
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    mask = np.triu(np.ones((seq, seq), dtype=bool), 1) if causal else None
+    for b in range(batch):
+        for h in range(hq):
+            kh, vh = k[b, :, h // group], v[b, :, h // group]
+            z = q[b, :, h] @ kh.T * scale
+            if mask is not None:
+                z = np.where(mask, -np.inf, z)
+            z = z - z.max(axis=-1, keepdims=True)
+            p = np.exp(z)
+            p /= p.sum(axis=-1, keepdims=True)
+            o = p @ vh
+            gh = g[b, :, h]
+            dv[b, :, h // group] += p.T @ gh
+            dp = gh @ vh.T
+            dz = p * (dp - np.sum(gh * o, axis=-1, keepdims=True))
+            dq[b, :, h] = scale * dz @ kh
+            dk[b, :, h // group] += scale * dz.T @ q[b, :, h]
+    return dq, dk, dv
+
+
+def attention_varlen_bwd(q, k, v, do, cu_seqlens, causal: bool = False, scale: float | None = None):
+    """Gradients of `attention_varlen` (dq, dk, dv), segment by segment."""
+    q, k, v, g = _f64(q), _f64(k), _f64(v), _f64(do)
+    bounds = [int(c) for c in np.asarray(cu_seqlens).tolist()]
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for lo, hi in zip(bounds, bounds[1:]):
+        if hi == lo:
+            continue
+        a, b_, c = attention_bwd(q[None, lo:hi], k[None, lo:hi], v[None, lo:hi], g[None, lo:hi], causal, scale)
+        dq[lo:hi], dk[lo:hi], dv[lo:hi] = a[0], b_[0], c[0]
+    return dq, dk, dv

@@ -109,15 +109,14 @@ def attn_varlen_supported(q, k, v, cu_seqlens, causal, softmax_scale) -> bool:
     )
 
 
-# (op, source, predicate, forward_only): attention has no backward kernel yet,
-# so Popcorn declines it whenever a call needs gradients.
+# (op, source, predicate, forward_only): every op has its backward kernels.
 REGISTRATIONS = (
     ("rms_norm", "popcorn_amd.impls.rms_norm", rms_norm_supported, False),
     ("add_rms_norm", "popcorn_amd.impls.add_rms_norm", add_rms_norm_supported, False),
     ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
     ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
-    ("attn", "popcorn_amd.impls.attn", attn_supported, True),
-    ("attn_varlen", "popcorn_amd.impls.attn_varlen", attn_varlen_supported, True),
+    ("attn", "popcorn_amd.impls.attn", attn_supported, False),
+    ("attn_varlen", "popcorn_amd.impls.attn_varlen", attn_varlen_supported, False),
 )
 
 

@@ -1,0 +1,49 @@
+// Pieces shared by the attention kernels: matrix-core fragment types, the
+// 32x32x16 MFMA for each 16-bit element type, and 16-byte buffer loads.
+#pragma once
+
+#include "common.h"
+
+namespace pk {
+namespace attn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s4;
+
+// D[32x32] += A[32x16] B[16x32]: lane l holds row l%32 of A (K elements
+// 8*(l/32) .. +8) and column l%32 of B (the same K elements); the result
+// lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mma<f16> {
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16 bytes at voffset + soffset of a buffer resource (zeros past its range)
+__device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Four 16-bit values as two packed 32-bit words
+template <typename T> __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  return make_uint2((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(a)) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(b)) << 16),
+                    (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(c)) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(d)) << 16));
+}
+
+}  // namespace attn
+}  // namespace pk

@@ -57,34 +57,16 @@
 #include <type_traits>
 
 #include "api.h"
-#include "common.h"
+#include "attn_common.h"
 
 namespace pk {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s4;
+using namespace attn;
 
 constexpr int BM = 128;
 constexpr int BN = 32;
 constexpr int NT = 256;
-
-template <typename T> struct Mma;
-template <> struct Mma<bf16> {
-  typedef bf16x8 frag;
-  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct Mma<f16> {
-  typedef f16x8 frag;
-  static __device__ __forceinline__ f32x16 run(frag a, frag b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-};
 
 // Largest row sum the fixed-max sweep accepts (see the header).
 template <typename T> constexpr float kFastLimit = 4294967296.0f;
@@ -106,12 +88,6 @@ struct AttnArgs {
   float c;          // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
-
-__device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
-  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_fwd_kernel(

@@ -11,9 +11,9 @@ host-side or torch fallback: an input the kernels do not cover raises.
     add_rms_norm(x, residual, weight, eps=1e-6, offset=0.0)  kernels/add_rms_norm.py:8-26
     swiglu(a, b)                                    kernels/swiglu.py:9-18
     rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
-    attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37 (forward only)
+    attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37
     attn_varlen(q, k, v, cu_seqlens, causal=False, softmax_scale=None)
-                                                    kernels/attn_varlen.py:15-54 (forward only)
+                                                    kernels/attn_varlen.py:15-54
 """
 
 from __future__ import annotations
@@ -337,57 +337,79 @@ def rotary_embedding_(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = F
 def attn_with_lse(
     q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None
 ) -> tuple[Tensor, Tensor]:
-    """Forward attention returning (o [batch, seq, q_heads, head_dim], lse [batch, q_heads, seq] fp32)."""
-    return _attention(q, k, v, causal, softmax_scale, want_lse=True)
+    """Forward attention returning (o [batch, seq, q_heads, head_dim], lse [batch, q_heads, seq] fp32); no autograd."""
+    return _attn_fwd(q, k, v, causal, softmax_scale, want_lse=True)
 
 
 def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None) -> Tensor:
-    """softmax(q k^T * scale + causal mask) v with grouped kv heads; forward only.
+    """softmax(q k^T * scale + causal mask) v with grouped kv heads.
 
     q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim];
     bf16 or fp16; head_dim 64 or 128; scale defaults to head_dim ** -0.5.
+    Backward gives dq, dk, dv.
     """
-    return _attention(q, k, v, causal, softmax_scale, want_lse=False)[0]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _Attention.apply(q, k, v, causal, softmax_scale)
+    return _attn_fwd(q, k, v, causal, softmax_scale, want_lse=False)[0]
 
 
-def _attention(q, k, v, causal, softmax_scale, want_lse):
+def _scale(head_dim: int, softmax_scale: float | None) -> float:
+    return head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+
+
+def _attn_fwd(q, k, v, causal, softmax_scale, want_lse):
     device = _require_cuda(q, k, v)
     dtype = _same_dtype("attn", q, k, v)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        raise RuntimeError("popcorn_amd.attn is forward-only; call it under torch.no_grad() or on detached inputs")
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
         raise ValueError("popcorn_amd.attn: q [b, s, hq, d] and k, v [b, s, hkv, d] expected")
     batch, seq, q_heads, head_dim = q.shape
     if k.shape[0] != batch or k.shape[1] != seq or k.shape[3] != head_dim:
         raise ValueError(f"popcorn_amd.attn: k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
     kv_heads = k.shape[2]
-    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
-    q_, k_, v_ = (_aligned_rows(t) for t in (q, k, v))
+    q_, k_, v_ = (_aligned_rows(t.detach()) for t in (q, k, v))
     o = torch.empty((batch, seq, q_heads, head_dim), dtype=dtype, device=device)
     lse = torch.empty((batch, q_heads, seq), dtype=torch.float32, device=device) if want_lse else None
     lib = _lib.load()
     strides = (_lib._i64 * 12)(*(s for t in (q_, k_, v_, o) for s in t.stride()[:3]))
     _lib.check(
         lib.pk_attn_fwd(
-            q_.data_ptr(),
-            k_.data_ptr(),
-            v_.data_ptr(),
-            o.data_ptr(),
-            lse.data_ptr() if lse is not None else None,
-            strides,
-            batch,
-            seq,
-            q_heads,
-            kv_heads,
-            head_dim,
-            scale,
-            int(bool(causal)),
-            _lib.dtype_code(dtype),
-            _lib.stream_handle(device),
+            q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
+            strides, batch, seq, q_heads, kv_heads, head_dim, _scale(head_dim, softmax_scale), int(bool(causal)),
+            _lib.dtype_code(dtype), _lib.stream_handle(device),
         ),
         lib,
     )
     return o, lse
+
+
+class _Attention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, causal, softmax_scale):
+        o, lse = _attn_fwd(q, k, v, causal, softmax_scale, want_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.causal, ctx.softmax_scale = bool(causal), softmax_scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        batch, seq, q_heads, head_dim = q.shape
+        q_, k_, v_, do_ = (_aligned_rows(t) for t in (q, k, v, do.to(q.dtype)))
+        dq, dk, dv = torch.empty(q.shape, dtype=q.dtype, device=q.device), torch.empty_like(k_), torch.empty_like(v_)
+        dk, dv = dk.contiguous(), dv.contiguous()
+        dsum = torch.empty_like(lse)
+        lib = _lib.load()
+        strides = (_lib._i64 * 24)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:3]))
+        _lib.check(
+            lib.pk_attn_bwd(
+                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
+                dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), strides, batch, seq, q_heads,
+                k.shape[2], head_dim, _scale(head_dim, ctx.softmax_scale), int(ctx.causal), _lib.dtype_code(q.dtype),
+                _lib.stream_handle(q.device),
+            ),
+            lib,
+        )
+        return dq, dk, dv, None, None
 
 
 def _aligned_rows(t: Tensor) -> Tensor:
@@ -399,23 +421,28 @@ def _aligned_rows(t: Tensor) -> Tensor:
 def attn_varlen_with_lse(
     q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, causal: bool = False, softmax_scale: float | None = None
 ) -> tuple[Tensor, Tensor]:
-    """Packed-sequence attention returning (o [total, q_heads, head_dim], lse [q_heads, total] fp32)."""
-    return _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse=True)
+    """Packed-sequence attention returning (o [total, q_heads, head_dim], lse [q_heads, total] fp32); no autograd."""
+    cu, num_seqs, longest = _cut_points(cu_seqlens, q.shape[0], q.device)
+    return _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=True)
 
 
 def attn_varlen(
     q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, causal: bool = False, softmax_scale: float | None = None
 ) -> Tensor:
-    """Attention over packed variable-length sequences, each attended independently; forward only.
+    """Attention over packed variable-length sequences, each attended independently.
 
     q [total, q_heads, head_dim], k, v [total, kv_heads, head_dim]; cu_seqlens
     int32 [num_seqs + 1] offsets from 0 to total (the flash-attention varlen
-    layout). Causal masks are top-left aligned within each sequence.
+    layout). Causal masks are top-left aligned within each sequence. Backward
+    gives dq, dk, dv.
     """
-    return _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse=False)[0]
+    cu, num_seqs, longest = _cut_points(cu_seqlens, q.shape[0], q.device)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _AttentionVarlen.apply(q, k, v, cu, num_seqs, longest, causal, softmax_scale)
+    return _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=False)[0]
 
 
-def _cut_points(cu_seqlens: Tensor, total: int) -> tuple[Tensor, int, int]:
+def _cut_points(cu_seqlens: Tensor, total: int, device: torch.device) -> tuple[Tensor, int, int]:
     """(cu_seqlens as an int32 device tensor, number of sequences, longest sequence); one host read."""
     if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2 or cu_seqlens.is_floating_point():
         raise ValueError("popcorn_amd.attn_varlen: cu_seqlens must be a 1-D integer tensor of num_seqs + 1 offsets")
@@ -423,24 +450,18 @@ def _cut_points(cu_seqlens: Tensor, total: int) -> tuple[Tensor, int, int]:
     if cuts[0] != 0 or cuts[-1] != total or any(b < a for a, b in zip(cuts, cuts[1:])):
         raise ValueError(f"popcorn_amd.attn_varlen: cu_seqlens must rise from 0 to total={total}, got {cuts[:8]}...")
     longest = max(b - a for a, b in zip(cuts, cuts[1:]))
-    return cu_seqlens, len(cuts) - 1, longest
+    return cu_seqlens.to(device=device, dtype=torch.int32).contiguous(), len(cuts) - 1, longest
 
 
-def _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse):
+def _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse):
     device = _require_cuda(q, k, v)
     dtype = _same_dtype("attn_varlen", q, k, v)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        raise RuntimeError("popcorn_amd.attn_varlen is forward-only; call it under torch.no_grad() or on detached inputs")
     if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape:
         raise ValueError("popcorn_amd.attn_varlen: q [total, hq, d] and k, v [total, hkv, d] expected")
     total, q_heads, head_dim = q.shape
     if k.shape[0] != total or k.shape[2] != head_dim:
         raise ValueError(f"popcorn_amd.attn_varlen: k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
-    cu, num_seqs, longest = _cut_points(cu_seqlens, total)
-    cu = cu.to(device=device, dtype=torch.int32).contiguous()
-    kv_heads = k.shape[1]
-    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
-    q_, k_, v_ = (_aligned_rows(t) for t in (q, k, v))
+    q_, k_, v_ = (_aligned_rows(t.detach()) for t in (q, k, v))
     o = torch.empty((total, q_heads, head_dim), dtype=dtype, device=device)
     lse = torch.empty((q_heads, total), dtype=torch.float32, device=device) if want_lse else None
     lib = _lib.load()
@@ -448,9 +469,41 @@ def _attention_varlen(q, k, v, cu_seqlens, causal, softmax_scale, want_lse):
     _lib.check(
         lib.pk_attn_varlen_fwd(
             q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
-            cu.data_ptr(), strides, num_seqs, total, longest, q_heads, kv_heads, head_dim, scale, int(bool(causal)),
-            _lib.dtype_code(dtype), _lib.stream_handle(device),
+            cu.data_ptr(), strides, num_seqs, total, longest, q_heads, k.shape[1], head_dim,
+            _scale(head_dim, softmax_scale), int(bool(causal)), _lib.dtype_code(dtype), _lib.stream_handle(device),
         ),
         lib,
     )
     return o, lse
+
+
+class _AttentionVarlen(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu, num_seqs, longest, causal, softmax_scale):
+        o, lse = _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse, cu)
+        ctx.meta = (num_seqs, longest, bool(causal), softmax_scale)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, cu = ctx.saved_tensors
+        num_seqs, longest, causal, softmax_scale = ctx.meta
+        total, q_heads, head_dim = q.shape
+        q_, k_, v_, do_ = (_aligned_rows(t) for t in (q, k, v, do.to(q.dtype)))
+        dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+        dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        dsum = torch.empty_like(lse)
+        lib = _lib.load()
+        strides = (_lib._i64 * 16)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:2]))
+        _lib.check(
+            lib.pk_attn_varlen_bwd(
+                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
+                dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), strides, num_seqs,
+                total, longest, q_heads, k.shape[1], head_dim, _scale(head_dim, softmax_scale), int(causal),
+                _lib.dtype_code(q.dtype), _lib.stream_handle(q.device),
+            ),
+            lib,
+        )
+        return dq, dk, dv, None, None, None, None, None

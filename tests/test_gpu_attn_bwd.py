@@ -1,0 +1,141 @@
+"""Attention backward (dense and packed) on the GPU against the float64 oracle and Popcorn's reference.
+
+The native-dtype reference gradients come from torch autograd of the
+registered reference on the CPU (its GPU path would issue batched 16-bit
+products on transposed views).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as O
+from popcorn_amd import impls
+from popcorn_amd.compat import references as R
+from tests._parity import gauge_ok, seeded
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def _grads(fn, inputs, do):
+    leaves = [t.clone().requires_grad_() for t in inputs]
+    out = fn(*leaves)
+    return out, torch.autograd.grad(out, leaves, do)
+
+
+def _check(batch, seq, hq, hkv, d, causal, scale, dtype, seed=0):
+    q = seeded((batch, seq, hq, d), seed, dtype)
+    k = seeded((batch, seq, hkv, d), seed + 1, dtype)
+    v = seeded((batch, seq, hkv, d), seed + 2, dtype)
+    do = seeded((batch, seq, hq, d), seed + 3, dtype)
+    truth = O.attention_bwd(*(t.double().numpy() for t in (q, k, v, do)), causal, scale)
+    _, ref = _grads(lambda a, b, c: R.attn(a, b, c, causal, scale), (q, k, v), do)
+    om, mine = _grads(lambda a, b, c: impls.attn(a, b, c, causal, scale), (q.to(DEV), k.to(DEV), v.to(DEV)),
+                      do.to(DEV))
+    o64, _ = O.attention(q.double().numpy(), k.double().numpy(), v.double().numpy(), causal, scale)
+    gauge_ok(om, o64, R.attn(q, k, v, causal, scale), dtype, "o")
+    for name, got, want, r in zip(("dq", "dk", "dv"), mine, truth, ref):
+        assert got.shape == r.shape and got.dtype == dtype
+        gauge_ok(got, want, r, dtype, f"{name} (seq {seq}, d {d}, causal {causal}, scale {scale})")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("seq", [1, 17, 64, 130, 257])
+def test_attn_bwd_shapes(seq, causal, d, dtype):
+    _check(2, seq, 8, 2, d, causal, None, dtype)
+
+
+@pytest.mark.parametrize("hkv", [8, 4, 1])
+@pytest.mark.parametrize("scale", [None, 0.25])
+def test_attn_bwd_groups_and_scale(hkv, scale):
+    _check(1, 200, 8, hkv, 128, True, scale, torch.bfloat16, seed=7)
+
+
+def test_attn_bwd_negative_scale():
+    """A negative scale negates q on load in the kernels: dk uses |scale|, dq the signed one."""
+    _check(1, 96, 4, 2, 128, False, -0.3, torch.bfloat16, seed=9)
+
+
+def test_attn_bwd_noncontiguous_inputs_and_cotangent():
+    b, s, hq, hkv, d = 2, 130, 8, 2, 128
+    packed = seeded((b, s, hq + 2 * hkv, d), 11, torch.bfloat16).to(DEV)
+    do_full = seeded((b, s, 2 * hq, d), 12, torch.bfloat16).to(DEV)
+    do = do_full[:, :, ::2]  # stride-2 heads
+    q, k, v = packed[:, :, :hq], packed[:, :, hq:hq + hkv], packed[:, :, hq + hkv:]
+    leaves = [t.detach().clone().requires_grad_() for t in (q, k, v)]
+    mine = torch.autograd.grad(impls.attn(*leaves, True), leaves, do)
+    dense = [t.contiguous().requires_grad_() for t in (q.detach(), k.detach(), v.detach())]
+    again = torch.autograd.grad(impls.attn(*dense, True), dense, do.contiguous())
+    for a, b_ in zip(mine, again):
+        assert torch.equal(a, b_)
+
+
+def _check_varlen(total, segments, d, causal, dtype, seed=0):
+    cu = R.cuts(torch.zeros(segments + 1, dtype=torch.int64), {"total": total}, torch.Generator().manual_seed(seed))
+    hq, hkv = 8, 2
+    q = seeded((total, hq, d), seed, dtype)
+    k = seeded((total, hkv, d), seed + 1, dtype)
+    v = seeded((total, hkv, d), seed + 2, dtype)
+    do = seeded((total, hq, d), seed + 3, dtype)
+    truth = O.attention_varlen_bwd(*(t.double().numpy() for t in (q, k, v, do)), cu.numpy(), causal)
+    _, ref = _grads(lambda a, b, c: R.attn_varlen(a, b, c, cu, causal), (q, k, v), do)
+    _, mine = _grads(lambda a, b, c: impls.attn_varlen(a, b, c, cu.to(DEV), causal),
+                     (q.to(DEV), k.to(DEV), v.to(DEV)), do.to(DEV))
+    for name, got, want, r in zip(("dq", "dk", "dv"), mine, truth, ref):
+        gauge_ok(got, want, r, dtype, f"{name} (varlen {cu.tolist()[:6]}, d {d}, causal {causal})")
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("total,segments", [(37, 1), (300, 3), (700, 7), (129, 129)])
+def test_attn_varlen_bwd(total, segments, d, causal):
+    _check_varlen(total, segments, d, causal, torch.bfloat16)
+
+
+def test_attn_varlen_bwd_fp16():
+    _check_varlen(500, 4, 128, True, torch.float16, seed=5)
+
+
+def test_attn_varlen_bwd_equal_segments_match_dense():
+    b, s, hq, hkv, d = 3, 200, 8, 2, 128
+    q, k, v, do = (seeded((b, s, h, d), i, torch.bfloat16).to(DEV) for i, h in enumerate((hq, hkv, hkv, hq)))
+    cu = torch.arange(0, (b + 1) * s, s, dtype=torch.int32, device=DEV)
+    for causal in (False, True):
+        ld = [t.clone().requires_grad_() for t in (q, k, v)]
+        gd = torch.autograd.grad(impls.attn(*ld, causal), ld, do)
+        lv = [t.reshape(b * s, t.shape[2], d).clone().requires_grad_() for t in (q, k, v)]
+        gv = torch.autograd.grad(impls.attn_varlen(*lv, cu, causal), lv, do.reshape(b * s, hq, d))
+        for a, c in zip(gd, gv):
+            assert torch.equal(a, c.reshape(a.shape))
+
+
+def test_attn_bwd_long_causal_against_float64_on_device():
+    """B=1, S=4096, Hq=16, Hkv=4, D=128 causal bf16: one kv group's dq / dk / dv against float64 autograd."""
+    b, s, hq, hkv, d = 1, 4096, 16, 4, 128
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(b, s, hkv, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    dq, dk, dv = torch.autograd.grad(impls.attn(*leaves, True), leaves, do)
+    grp = 2  # kv head 2 and its q heads 8..11
+    qh = q[0, :, 4 * grp:4 * grp + 4].double().permute(1, 0, 2).requires_grad_()
+    kh = k[0, :, grp].double().requires_grad_()
+    vh = v[0, :, grp].double().requires_grad_()
+    z = (qh @ kh.T) * d**-0.5
+    z = z.masked_fill(torch.ones(s, s, dtype=torch.bool, device=DEV).triu(1), float("-inf"))
+    o = torch.softmax(z, -1) @ vh
+    gq, gk, gv = torch.autograd.grad(o, (qh, kh, vh), do[0, :, 4 * grp:4 * grp + 4].double().permute(1, 0, 2))
+    for name, got, want in (("dq", dq[0, :, 4 * grp:4 * grp + 4].permute(1, 0, 2), gq), ("dk", dk[0, :, grp], gk),
+                            ("dv", dv[0, :, grp], gv)):
+        err = (got.double() - want).abs().max().item()
+        scale = max(1.0, want.abs().max().item())
+        assert err <= 2e-2 * scale, f"{name}: {err:.3e} vs {scale:.2f}"

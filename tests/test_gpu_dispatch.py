@@ -99,29 +99,29 @@ def test_rotary_records_and_routes():
     _check_record_and_route(op, record, lambda: op(x, cos, sin))
 
 
-def test_attn_forward_only_records_and_routes():
+def test_attn_records_and_routes_with_grad():
     op = compat.KERNELS["attn"]
     q, k, v = _randn(1, 1024, 8, 128), _randn(1, 1024, 2, 128, seed=1), _randn(1, 1024, 2, 128, seed=2)
     with torch.no_grad():
         [record] = op.benchmark(q, k, v, True, backend=NAME)
         assert not record.result.grad
         _check_record_and_route(op, record, lambda: op(q, k, v, True))
-    # a call that needs gradients is declined by the forward-only backend
-    qg = q.clone().requires_grad_()
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
     op.tuner.forget()
-    op(qg, k, v, True)
-    assert _selected(op) == "torch"
+    [record] = op.benchmark(qg, kg, vg, True, backend=NAME)
+    assert record.result.grad and {"q", "k", "v"} <= set(record.result.bwd)
+    _check_record_and_route(op, record, lambda: op(qg, kg, vg, True))
 
 
-def test_attn_varlen_forward_only_records_and_routes():
+def test_attn_varlen_records_and_routes_with_grad():
     op = compat.KERNELS["attn_varlen"]
     total = 3000
     q, k, v = _randn(total, 8, 128), _randn(total, 2, 128, seed=1), _randn(total, 2, 128, seed=2)
     cu = torch.tensor([0, 1000, 1001, 2500, total], dtype=torch.int32, device=DEV)
-    with torch.no_grad():
-        [record] = op.benchmark(q, k, v, cu, True, backend=NAME)
-        assert not record.result.grad
-        _check_record_and_route(op, record, lambda: op(q, k, v, cu, True))
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    [record] = op.benchmark(qg, kg, vg, cu, True, backend=NAME)
+    assert record.result.grad
+    _check_record_and_route(op, record, lambda: op(qg, kg, vg, cu, True))
 
 
 def test_mixed_dtype_rotary_is_served_in_registration_order():

@@ -361,6 +361,68 @@ def test_attention_varlen_segments_are_independent():
         np.testing.assert_allclose(o[lo:hi], want, rtol=1e-12, atol=1e-12)
 
 
+# --------------------------------------------------------------------------- attention backward
+
+
+def test_attention_bwd_matches_torch_autograd():
+    r = rng(61)
+    q, do = r.standard_normal((2, 9, 4, 8)), r.standard_normal((2, 9, 4, 8))
+    k, v = r.standard_normal((2, 9, 2, 8)), r.standard_normal((2, 9, 2, 8))
+    # (torch's SDPA gives NaN for a negative scale under its causal mask, so that sign is checked unmasked)
+    for causal, scale in ((False, None), (True, 0.3), (False, -0.5)):
+        qt, kt, vt = (torch.from_numpy(t).requires_grad_() for t in (q, k, v))
+        out = F.scaled_dot_product_attention(qt.transpose(1, 2), kt.repeat_interleave(2, 2).transpose(1, 2),
+                                             vt.repeat_interleave(2, 2).transpose(1, 2), is_causal=causal,
+                                             scale=scale).transpose(1, 2)
+        gq, gk, gv = torch.autograd.grad(out, (qt, kt, vt), torch.from_numpy(do))
+        dq, dk, dv = O.attention_bwd(q, k, v, do, causal, scale)
+        np.testing.assert_allclose(dq, gq.numpy(), rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(dk, gk.numpy(), rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(dv, gv.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_attention_bwd_finite_differences():
+    r = rng(62)
+    q, do = r.standard_normal((1, 4, 2, 3)), r.standard_normal((1, 4, 2, 3))
+    k, v = r.standard_normal((1, 4, 1, 3)), r.standard_normal((1, 4, 1, 3))
+    h = 1e-6
+    dq, dk, dv = O.attention_bwd(q, k, v, do, True, 0.7)
+
+    def loss(qq, kk, vv):
+        return float(np.sum(O.attention(qq, kk, vv, True, 0.7)[0] * do))
+
+    for grad, which in ((dq, 0), (dk, 1), (dv, 2)):
+        args = [q, k, v]
+        base = args[which]
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            plus, minus = base.copy(), base.copy()
+            plus[idx] += h
+            minus[idx] -= h
+            ap, am = list(args), list(args)
+            ap[which], am[which] = plus, minus
+            num[idx] = (loss(*ap) - loss(*am)) / (2 * h)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-8)
+
+
+def test_attention_bwd_zero_scale_and_varlen():
+    r = rng(63)
+    q, do = r.standard_normal((1, 6, 2, 4)), r.standard_normal((1, 6, 2, 4))
+    k, v = r.standard_normal((1, 6, 2, 4)), r.standard_normal((1, 6, 2, 4))
+    dq, dk, dv = O.attention_bwd(q, k, v, do, False, 0.0)  # uniform attention: no dependence on q or k
+    assert np.abs(dq).max() == 0 and np.abs(dk).max() == 0
+    np.testing.assert_allclose(dv[0, :, 0], np.broadcast_to(do[0, :, 0].mean(0), (6, 4)), rtol=1e-12)
+    # varlen: two segments equal the dense backward of each segment
+    cu = [0, 2, 6]
+    vq, vk, vv, vdo = q[0], k[0], v[0], do[0]
+    dqv, dkv, dvv = O.attention_varlen_bwd(vq, vk, vv, vdo, cu, True, 0.5)
+    for lo, hi in zip(cu, cu[1:]):
+        a, b_, c = O.attention_bwd(q[:, lo:hi], k[:, lo:hi], v[:, lo:hi], do[:, lo:hi], True, 0.5)
+        np.testing.assert_array_equal(dqv[lo:hi], a[0])
+        np.testing.assert_array_equal(dkv[lo:hi], b_[0])
+        np.testing.assert_array_equal(dvv[lo:hi], c[0])
+
+
 # --------------------------------------------------------------------------- planted mistakes
 
 
