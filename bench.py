@@ -6,8 +6,9 @@ A step is one pass of a workload's drop-in call (the `popcorn_amd.impls`
 function Popcorn dispatches to) over one batch of synthetic input already
 resident in HBM. The default workload is BASELINE config 2 (SwiGLU forward,
 bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, `add_rmsnorm`
-(residual add + RMSNorm at C4's shape, the next op on the norm path), or
-`copy`, a plain device copy of known size used to calibrate HBM byte counters.
+(residual add + RMSNorm at C4's shape), `attn_bwd` (attention forward +
+backward at C5's shape), or `copy`, a plain device copy of known size used to
+calibrate HBM byte counters.
 
 Rank 0 prints ONE JSON line. `value` is the workload's achieved algorithmic
 throughput (TB/s of HBM bytes for c1-c4, TFLOP/s for c5). `roofline` is the
@@ -49,6 +50,7 @@ MEASURED_TRAFFIC: dict[str, int | None] = {
     "c4": 3_240_299_913,
     "c5": 2_632_999_026,
     "add_rmsnorm": 4_314_051_694,
+    "attn_bwd": 15_115_471_835,  # the dq and dk/dv kernels of one pk_attn_bwd call
     "copy": 1_073_766_308,
 }
 
@@ -275,6 +277,51 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                         "bf16", "TB/s", fwd_bytes + bwd_bytes, step, "rmsnorm_bwd_vec", bwd_bytes, launch,
                         {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu)
 
+    if name == "attn_bwd":
+        # not a BASELINE config: attention forward + backward at C5's shape (bf16, causal)
+        B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
+        q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
+        k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        do = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
+        fwd_flops = 4.0 * B * HQ * D * S * S / 2
+        bwd_flops = 2.5 * fwd_flops  # the customary count: dQ, dK, dV, dP and S recomputed once (5 products)
+        qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
+        o, lse = impls.attn_with_lse(q, k, v, True)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dsum = torch.empty_like(lse)
+        strides = (_lib._i64 * 24)(*(s for t in (q, k, v, o, do, dq, dk, dv) for s in t.stride()[:3]))
+
+        def step(i):
+            out = impls.attn(qg, kg, vg, True)
+            torch.autograd.grad(out, (qg, kg, vg), do)
+
+        def launch(i):
+            _lib.check(lib.pk_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                                       lse.data_ptr(), dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            sq = 1024  # one (batch, kv group) of 1024 tokens; work scaled to that
+            qc = torch.randn(1, sq, 4, D).bfloat16().requires_grad_()
+            kc, vc = (torch.randn(1, sq, 1, D).bfloat16().requires_grad_() for _ in range(2))
+            gc = torch.randn(1, sq, 4, D).bfloat16()
+
+            def one():
+                oc = R.attn(qc, kc, vc, True)
+                torch.autograd.grad(oc, (qc, kc, vc), gc)
+
+            t, reps = _time_cpu(one)
+            work = 3.5 * 4.0 * 4 * D * sq * sq / 2
+            return work / t / 1e12, f"B=1, S={sq}, Hq=4, Hkv=1 causal fwd+bwd bf16, median of {reps} reps"
+
+        return Workload("attn_bwd", "Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16",
+                        "TFLOP/s", fwd_flops + bwd_flops, step, "attn_bwd", bwd_flops, launch,
+                        {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
+                         "dtype": "bf16"}, cpu)
+
     if name == "c5":
         B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
         q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
@@ -321,7 +368,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         return Workload("copy", "plain device copy, 512 MiB -> 512 MiB", "bf16", "TB/s", nbytes, step, "copy",
                         nbytes, step, {"bytes_each_way": numel * 2})
 
-    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, copy)")
+    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, attn_bwd, copy)")
 
 
 def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 20) -> tuple[float, int]:
@@ -397,7 +444,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "attn_bwd", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
     args = ap.parse_args(argv)
