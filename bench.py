@@ -50,6 +50,7 @@ MEASURED_TRAFFIC: dict[str, int | None] = {
     "c4": 3_240_299_913,
     "c5": 2_632_999_026,
     "add_rmsnorm": 4_314_051_694,
+    "rope": 337_726_126,
     "attn_bwd": 15_115_471_835,  # the dq and dk/dv kernels of one pk_attn_bwd call
     "copy": 1_073_766_308,
 }
@@ -179,6 +180,54 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                         "bf16", "TB/s", nbytes, step, "rotary_kernel", 2 * qb + table, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "theta": 500000.0,
                          "dtype": "bf16", "tables": "fp32"}, cpu)
+
+    if name == "rope":
+        # not a BASELINE config: paired q/k rope at the shape of the notebook's fused qk-norm+rope example
+        B, HQ, HKV, S, D = 4, 32, 8, 4096, 128
+        inv_freq = 500000.0 ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+        ang = torch.arange(S, dtype=torch.float64)[:, None] * inv_freq[None, :]
+        ang = torch.cat([ang, ang], -1)[None]
+        cos, sin = ang.cos().bfloat16().to(dev), ang.sin().bfloat16().to(dev)
+        qb, kb = B * HQ * S * D * 2, B * HKV * S * D * 2
+        launch_bytes = 2 * (qb + kb) + 2 * S * D * 2
+        n = _copies(launch_bytes)
+        qs = [_randn((B, HQ, S, D), torch.bfloat16, gen, dev) for _ in range(n)]
+        ks = [_randn((B, HKV, S, D), torch.bfloat16, gen, dev) for _ in range(n)]
+        gq, gk = _randn((B, HQ, S, D), torch.bfloat16, gen, dev), _randn((B, HKV, S, D), torch.bfloat16, gen, dev)
+        leaves = [(q.requires_grad_(), k.requires_grad_()) for q, k in zip(qs, ks)]
+        yq, yk = torch.empty_like(qs[0]), torch.empty_like(ks[0])
+        strides = (_lib._i64 * 12)(*(x for t in (qs[0], ks[0], yq, yk) for x in t.stride()[:3]))
+
+        def step(i):
+            q, k = leaves[i % n]
+            oq, ok = impls.rope(q, k, cos, sin)
+            torch.autograd.grad((oq, ok), (q, k), (gq, gk))
+
+        def launch(i):
+            q, k = qs[i % n], ks[i % n]
+            _lib.check(lib.pk_rope(q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(), yq.data_ptr(),
+                                   yk.data_ptr(), strides, B, HQ, HKV, S, D, 1, _lib.BF16, _lib.BF16, 0, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            qc = torch.randn(1, HQ, S, D).bfloat16().requires_grad_()
+            kc = torch.randn(1, HKV, S, D).bfloat16().requires_grad_()
+            cc, sc = cos.cpu(), sin.cpu()
+            gqc, gkc = torch.randn(1, HQ, S, D).bfloat16(), torch.randn(1, HKV, S, D).bfloat16()
+
+            def one():
+                oq, ok = R.rope(qc, kc, cc, sc)
+                torch.autograd.grad((oq, ok), (qc, kc), (gqc, gkc))
+
+            t, reps = _time_cpu(one)
+            work = 2 * (2 * (qc.numel() + kc.numel()) * 2 + 2 * S * D * 2)
+            return work / t / 1e12, f"batch 1 of {B}, fwd+bwd, median of {reps} reps"
+
+        return Workload("rope", "rope fwd+bwd bf16 q [4,32,4096,128], k [4,8,4096,128], bf16 cos/sin [1,4096,128]",
+                        "bf16", "TB/s", 2 * launch_bytes, step, "rope_kernel", launch_bytes, launch,
+                        {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
+                         "theta": 500000.0, "dtype": "bf16"}, cpu)
 
     if name == "c4":
         rows, cols = 65536, 8192
@@ -444,7 +493,8 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "attn_bwd", "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "attn_bwd",
+                                                           "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
     args = ap.parse_args(argv)
@@ -471,7 +521,7 @@ def main(argv=None) -> int:
 
     others = {}
     if not args.no_others and wl.name != "copy":
-        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm"):
+        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope"):
             if name == wl.name:
                 continue
             del wl

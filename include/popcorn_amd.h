@@ -123,6 +123,22 @@ int pk_rotary(const void* x, const void* cos, const void* sin, void* y, const in
               int conjugate, void* stream);
 
 /*
+ * Paired rotary embedding of q [batch, q_heads, seq, head_dim] and
+ * k [batch, kv_heads, seq, head_dim] with full-width tables
+ * cos, sin [cos_batch, seq, head_dim] (contiguous; cos_batch 1 or batch):
+ *   y[j] = x[j] cos[j] - x[j+h] sin[j],  y[j+h] = x[j+h] cos[j+h] + x[j] sin[j+h]
+ * (h = head_dim/2), i.e. x*cos + rotate_half(x)*sin, fp32 arithmetic rounded
+ * once to x's dtype. transpose = 1 applies the adjoint map (the backward):
+ *   dx[j] = g[j] cos[j] + g[j+h] sin[j+h],  dx[j+h] = g[j+h] cos[j+h] - g[j] sin[j].
+ * strides[12] = q, k, yq, yk (batch, head, seq) strides in elements; the
+ * last dimension is contiguous. A side with zero heads may pass NULL.
+ * Replaces: reference `rope` (kernels/rope.py:19-36).
+ */
+int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void* yq, void* yk,
+            const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+            int64_t cos_batch, int x_dtype, int cs_dtype, int transpose, void* stream);
+
+/*
  * Attention forward, o = softmax(q k^T * scale + M) v, grouped-query:
  * q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim],
  * o like q; q head h reads kv head h / (q_heads / kv_heads). causal = 1 masks

@@ -26,6 +26,11 @@ independent fact that a plausible slip would break:
   swiglu_bwd        central finite differences; float64 autograd of F.silu
   rotary_embedding  complex multiplication (x1 + i x2)(c + i s); identity tables;
                     norm preservation for unit tables; conjugate inverts forward
+  rope              duplicated tables equal the NeoX rotary_embedding of q and k;
+                    cos = 1, sin = 0 is the identity; cos = 0, sin = 1 is rotate_half;
+                    explicit per-channel loops with unequal halves
+  rope_bwd          central finite differences; <rope(x), g> = <x, rope_bwd(g)>;
+                    duplicated unit tables: rope_bwd inverts rope
   attention         explicit per-query loops; float64 SDPA with repeat_interleave;
                     q = 0 gives prefix means of v and lse = log(t + 1); S = 1 gives v
   attention_bwd     float64 torch autograd of SDPA (repeat_interleave grouping);
@@ -165,6 +170,28 @@ def rotary_embedding(x, cos, sin, interleaved: bool = False) -> np.ndarray:
 def rotary_embedding_bwd(dy, cos, sin, interleaved: bool = False) -> np.ndarray:
     """dx of `rotary_embedding`: the transpose of the rotation, i.e. rotation by -sin."""
     return rotary_embedding(dy, cos, -_f64(sin), interleaved)
+
+
+def rope(q, k, cos, sin):
+    """Paired rotary embedding (kernels/rope.py:23-36): x*cos + rotate_half(x)*sin for x in (q, k).
+
+    q [B, Hq, S, D], k [B, Hkv, S, D], cos/sin [cos_batch, S, D] broadcast over
+    heads (cos_batch 1 or B); rotate_half(x) = (-x[h:], x[:h]) with h = D/2
+    (kernels/rope.py:8-10). The two halves of a table row may differ.
+    """
+    c, s = _f64(cos)[:, None], _f64(sin)[:, None]
+    return tuple(x * c + _rotate_half(x) * s for x in (_f64(q), _f64(k)))
+
+
+def rope_bwd(dq, dk, cos, sin):
+    """(dq_in, dk_in) of `rope`: the transpose g*cos + rotate_half^T(g*sin), rotate_half^T = -rotate_half."""
+    c, s = _f64(cos)[:, None], _f64(sin)[:, None]
+    return tuple(g * c - _rotate_half(g * s) for g in (_f64(dq), _f64(dk)))
+
+
+def _rotate_half(x: np.ndarray) -> np.ndarray:
+    h = x.shape[-1] // 2
+    return np.concatenate((-x[..., h:], x[..., :h]), axis=-1)
 
 
 def attention_rows(q, k, v, rows, causal: bool, scale: float | None = None):

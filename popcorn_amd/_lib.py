@@ -37,6 +37,7 @@ SIGNATURES = {
     "pk_add_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _int, _p]),
     "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _p]),
     "pk_rotary": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
+    "pk_rope": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _p]),
     "pk_attn_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_attn_bwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_attn_varlen_bwd": (_int, [_p] * 10 + [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),

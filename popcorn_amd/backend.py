@@ -83,6 +83,22 @@ def rotary_supported(x, cos, sin, interleaved) -> bool:
     )
 
 
+def rope_supported(q, k, cos, sin) -> bool:
+    return (
+        _on_hip(q, k, cos, sin)
+        and q.dtype in _FLOATS
+        and q.dtype == k.dtype == cos.dtype == sin.dtype
+        and q.dim() == k.dim() == 4
+        and cos.dim() == 3
+        and cos.shape == sin.shape
+        and q.shape[-1] % 2 == 0
+        and k.shape[0] == q.shape[0]
+        and k.shape[2:] == q.shape[2:]
+        and cos.shape[1:] == q.shape[2:]
+        and cos.shape[0] in (1, q.shape[0])
+    )
+
+
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:
     return (
         _on_hip(q, k, v)
@@ -115,6 +131,7 @@ REGISTRATIONS = (
     ("add_rms_norm", "popcorn_amd.impls.add_rms_norm", add_rms_norm_supported, False),
     ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
     ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
+    ("rope", "popcorn_amd.impls.rope", rope_supported, False),
     ("attn", "popcorn_amd.impls.attn", attn_supported, False),
     ("attn_varlen", "popcorn_amd.impls.attn_varlen", attn_varlen_supported, False),
 )

@@ -2,11 +2,12 @@
 
 Signatures, shape annotations and test-argument pools are Popcorn's
 (kernels/rms_norm.py:16-30, kernels/add_rms_norm.py:8-26, kernels/swiglu.py:9-18,
-kernels/rotary_embedding.py:12-40, kernels/attn.py:10-37,
+kernels/rotary_embedding.py:12-40, kernels/rope.py:19-36, kernels/attn.py:10-37,
 kernels/attn_varlen.py:15-54); the arithmetic is
 the eager-torch restatement in `popcorn_amd.compat.references`.
 """
 
+import torch
 from torch import Tensor
 
 from popcorn_amd.compat import references
@@ -52,6 +53,18 @@ def rotary_embedding(
 ) -> Float[Tensor, "batch seq heads head_dim"]:
     """Rotary position embedding, GPT-NeoX halves or GPT-J interleaved pairs."""
     return references.rotary_embedding(x, cos, sin, interleaved)
+
+
+@register_kernel(test_inputs={"cos": references.rope_table(torch.cos), "sin": references.rope_table(torch.sin)},
+                 tags={"positional"})
+def rope(
+    q: Float[Tensor, "batch q_heads seq head_dim"],
+    k: Float[Tensor, "batch kv_heads seq head_dim"],
+    cos: Float[Tensor, "cos_batch seq head_dim"],
+    sin: Float[Tensor, "cos_batch seq head_dim"],
+) -> tuple[Tensor, Tensor]:
+    """Paired rotary embedding of queries and keys: x*cos + rotate_half(x)*sin."""
+    return references.rope(q, k, cos, sin)
 
 
 @register_kernel(test_args={"softmax_scale": [None, 0.25]})

@@ -10,6 +10,7 @@ the native-dtype rounding the budget measures:
     add_rms_norm      kernels/add_rms_norm.py:8-26
     swiglu            kernels/swiglu.py:9-18
     rotary_embedding  kernels/rotary_embedding.py:12-40
+    rope              kernels/rope.py:8-36 (`_rotate_half`, `_table`: kernels/rope.py:8-14)
     attn              kernels/attn.py:10-37
     attn_varlen       kernels/attn_varlen.py:15-54 (`cuts`: kernels/_varlen.py:8-13)
 """
@@ -66,6 +67,26 @@ def rotary_embedding(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = Fa
     if 2 * half == x.shape[-1]:
         return rotated
     return torch.cat((rotated, x[..., 2 * half :]), dim=-1)
+
+
+def rotate_half(x: Tensor) -> Tensor:
+    """(x1, x2) -> (-x2, x1) over the last dimension's halves."""
+    x1, x2 = x.chunk(2, -1)
+    return torch.cat((-x2, x1), -1)
+
+
+def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+    """x*cos + rotate_half(x)*sin for x in (q, k), eager at the inputs' dtype (three roundings per output).
+
+    cos, sin [cos_batch, seq, head_dim] broadcast over heads and get no gradient.
+    """
+    cos, sin = cos.detach()[:, None], sin.detach()[:, None]
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def rope_table(f):
+    """Popcorn's rope test-input transform: f of the draw with its first half repeated over the row."""
+    return lambda t: f(t).chunk(2, -1)[0].repeat(1, 1, 2)
 
 
 def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: float | None = None) -> Tensor:

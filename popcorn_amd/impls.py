@@ -11,6 +11,7 @@ host-side or torch fallback: an input the kernels do not cover raises.
     add_rms_norm(x, residual, weight, eps=1e-6, offset=0.0)  kernels/add_rms_norm.py:8-26
     swiglu(a, b)                                    kernels/swiglu.py:9-18
     rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
+    rope(q, k, cos, sin)                            kernels/rope.py:19-36
     attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37
     attn_varlen(q, k, v, cu_seqlens, causal=False, softmax_scale=None)
                                                     kernels/attn_varlen.py:15-54
@@ -24,7 +25,7 @@ from torch import Tensor
 from popcorn_amd import _lib
 
 __all__ = ["rms_norm", "add_rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "attn_varlen",
-           "attn_varlen_with_lse", "rotary_embedding_"]
+           "attn_varlen_with_lse", "rotary_embedding_", "rope"]
 
 
 def _require_cuda(*tensors: Tensor | None) -> torch.device:
@@ -329,6 +330,69 @@ def rotary_embedding_(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = F
         raise ValueError("popcorn_amd.rotary_embedding_: last dimension must be contiguous")
     _rotate(x, cos.contiguous(), sin.contiguous(), x, interleaved, conjugate=False)
     return x
+
+
+def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpose: bool):
+    """One pk_rope launch over whichever of q, k is given; returns (yq, yk) (None for an absent side)."""
+    sides = [t for t in (q, k) if t is not None]
+    device = _require_cuda(*sides, cos, sin)
+    dtype = _same_dtype("rope", *sides, cos, sin)
+    if any(t.dim() != 4 for t in sides) or cos.dim() != 3 or cos.shape != sin.shape:
+        raise ValueError("popcorn_amd.rope: q [b, hq, s, d], k [b, hkv, s, d] and cos, sin [cos_batch, s, d] expected")
+    batch, _, seq, head_dim = sides[0].shape
+    for t in sides:
+        if t.shape[0] != batch or t.shape[2] != seq or t.shape[3] != head_dim:
+            raise ValueError(f"popcorn_amd.rope: q/k shapes {[tuple(t.shape) for t in sides]} disagree")
+    if cos.shape[1:] != (seq, head_dim) or cos.shape[0] not in (1, batch):
+        raise ValueError(f"popcorn_amd.rope: cos/sin {tuple(cos.shape)} must be [1 or {batch}, {seq}, {head_dim}]")
+    if head_dim % 2:
+        raise ValueError(f"popcorn_amd.rope: head_dim={head_dim} is odd")
+    xq, xk = (None if t is None else _last_contiguous(t.detach()) for t in (q, k))
+    yq, yk = (None if t is None else torch.empty(t.shape, dtype=dtype, device=device) for t in (q, k))
+    cs, sn = cos.detach().contiguous(), sin.detach().contiguous()
+
+    def strides(t):
+        return (0, 0, 0) if t is None else t.stride()[:3]
+
+    lib = _lib.load()
+    st = (_lib._i64 * 12)(*strides(xq), *strides(xk), *strides(yq), *strides(yk))
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    _lib.check(
+        lib.pk_rope(
+            ptr(xq), ptr(xk), cs.data_ptr(), sn.data_ptr(), ptr(yq), ptr(yk), st, batch,
+            0 if q is None else q.shape[1], 0 if k is None else k.shape[1], seq, head_dim, cos.shape[0],
+            _lib.dtype_code(dtype), _lib.dtype_code(dtype), int(transpose), _lib.stream_handle(device),
+        ),
+        lib,
+    )
+    return yq, yk
+
+
+class _Rope(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q: Tensor, k: Tensor, cos: Tensor, sin: Tensor):
+        yq, yk = _rope(q, k, cos, sin, transpose=False)
+        ctx.save_for_backward(cos.detach().contiguous(), sin.detach().contiguous())
+        return yq, yk
+
+    @staticmethod
+    def backward(ctx, gq: Tensor | None, gk: Tensor | None):
+        cos, sin = ctx.saved_tensors
+        if gq is None and gk is None:
+            return None, None, None, None
+        dq, dk = _rope(gq, gk, cos, sin, transpose=True)
+        return dq, dk, None, None
+
+
+def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
+    """Paired rotary embedding: (q*cos + rotate_half(q)*sin, k*cos + rotate_half(k)*sin).
+
+    q [batch, q_heads, seq, head_dim], k [batch, kv_heads, seq, head_dim],
+    cos, sin [cos_batch, seq, head_dim] with cos_batch 1 or batch, all one
+    dtype; the two halves of a table row may differ. fp32 arithmetic, one
+    rounding per output; one launch for q and k. cos and sin get no gradient.
+    """
+    return _Rope.apply(q, k, cos, sin)
 
 
 # --------------------------------------------------------------------------- attention

@@ -69,6 +69,14 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
     rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, 9, None)
     assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
+    rs = (ctypes.c_int64 * 12)(*([64] * 12))
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 63, 1, _lib.BF16, _lib.BF16, 0, None)
+    assert rc == _lib.ERR_INVALID and "odd" in lib.pk_last_error().decode()
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 3, _lib.BF16, _lib.BF16, 0, None)
+    assert rc == _lib.ERR_INVALID and "cos_batch" in lib.pk_last_error().decode()
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 2, _lib.BF16, _lib.BF16, 0, None)
+    assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
+    assert lib.pk_rope(None, None, None, None, None, None, rs, 2, 0, 0, 8, 64, 1, _lib.BF16, _lib.BF16, 0, None) == 0
 
 
 def test_missing_library_raises(tmp_path):

@@ -99,6 +99,16 @@ def test_rotary_records_and_routes():
     _check_record_and_route(op, record, lambda: op(x, cos, sin))
 
 
+def test_rope_records_and_routes_with_grad():
+    op = compat.KERNELS["rope"]
+    q, k = _randn(4, 32, 1024, 128).requires_grad_(), _randn(4, 8, 1024, 128, seed=1).requires_grad_()
+    ang = _randn(1, 1024, 64, dtype=torch.float32, seed=2)
+    cos, sin = (f(ang).repeat(1, 1, 2).bfloat16() for f in (torch.cos, torch.sin))
+    [record] = op.benchmark(q, k, cos, sin, backend=NAME)
+    assert record.result.grad and {"q", "k"} <= set(record.result.bwd)
+    _check_record_and_route(op, record, lambda: op(q, k, cos, sin))
+
+
 def test_attn_records_and_routes_with_grad():
     op = compat.KERNELS["attn"]
     q, k, v = _randn(1, 1024, 8, 128), _randn(1, 1024, 2, 128, seed=1), _randn(1, 1024, 2, 128, seed=2)

@@ -260,6 +260,72 @@ def test_rotary_bwd_is_transpose_by_finite_differences():
         np.testing.assert_allclose(O.rotary_embedding_bwd(g, c, s, il), _finite_diff(loss, x), rtol=1e-6, atol=1e-8)
 
 
+def _dup(t):
+    """[..., half] -> [..., 2*half] with the row repeated (Popcorn's rope table convention)."""
+    return np.concatenate([t, t], axis=-1)
+
+
+def test_rope_with_duplicated_tables_is_neox_rotary_of_q_and_k():
+    r = rng(15)
+    b, hq, hkv, seq, d = 2, 4, 2, 7, 16
+    q, k = r.standard_normal((b, hq, seq, d)), r.standard_normal((b, hkv, seq, d))
+    c, s = r.standard_normal((seq, d // 2)), r.standard_normal((seq, d // 2))
+    yq, yk = O.rope(q, k, _dup(c)[None], _dup(s)[None])
+    for x, y in ((q, yq), (k, yk)):
+        want = O.rotary_embedding(x.transpose(0, 2, 1, 3), c, s).transpose(0, 2, 1, 3)
+        np.testing.assert_allclose(y, want, rtol=1e-13, atol=1e-13)
+    # cos_batch = batch: each batch row uses its own table
+    cb, sb = r.standard_normal((b, seq, d // 2)), r.standard_normal((b, seq, d // 2))
+    yq, yk = O.rope(q, k, _dup(cb), _dup(sb))
+    for i in range(b):
+        want = O.rotary_embedding(q[i : i + 1].transpose(0, 2, 1, 3), cb[i], sb[i]).transpose(0, 2, 1, 3)
+        np.testing.assert_allclose(yq[i : i + 1], want, rtol=1e-13, atol=1e-13)
+
+
+def test_rope_identity_and_rotate_half_tables():
+    r = rng(16)
+    q, k = r.standard_normal((1, 3, 5, 8)), r.standard_normal((1, 1, 5, 8))
+    one, zero = np.ones((1, 5, 8)), np.zeros((1, 5, 8))
+    for x, y in zip((q, k), O.rope(q, k, one, zero)):
+        np.testing.assert_array_equal(y, x)
+    for x, y in zip((q, k), O.rope(q, k, zero, one)):
+        np.testing.assert_array_equal(y[..., :4], -x[..., 4:])
+        np.testing.assert_array_equal(y[..., 4:], x[..., :4])
+
+
+def test_rope_unequal_halves_by_explicit_loops():
+    r = rng(17)
+    b, h, seq, d = 2, 2, 3, 6
+    q, k = r.standard_normal((b, h, seq, d)), r.standard_normal((b, 1, seq, d))
+    c, s = r.standard_normal((b, seq, d)), r.standard_normal((b, seq, d))
+    yq, _ = O.rope(q, k, c, s)
+    half = d // 2
+    for i in range(b):
+        for hh in range(h):
+            for t in range(seq):
+                for j in range(d):
+                    partner = -q[i, hh, t, j + half] if j < half else q[i, hh, t, j - half]
+                    want = q[i, hh, t, j] * c[i, t, j] + partner * s[i, t, j]
+                    assert abs(yq[i, hh, t, j] - want) < 1e-14
+
+
+def test_rope_bwd_is_the_adjoint():
+    r = rng(18)
+    q, k = r.standard_normal((1, 2, 3, 8)), r.standard_normal((1, 1, 3, 8))
+    c, s = r.standard_normal((1, 3, 8)), r.standard_normal((1, 3, 8))
+    gq, gk = r.standard_normal(q.shape), r.standard_normal(k.shape)
+    dq, dk = O.rope_bwd(gq, gk, c, s)
+    loss = lambda: float(sum(np.sum(y * g) for y, g in zip(O.rope(q, k, c, s), (gq, gk))))  # noqa: E731
+    np.testing.assert_allclose(dq, _finite_diff(loss, q), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(dk, _finite_diff(loss, k), rtol=1e-6, atol=1e-8)
+    # unit duplicated tables: a rotation, so the adjoint inverts it
+    cu, su = _tables(3, 4)
+    cu, su = _dup(cu)[None], _dup(su)[None]
+    back = O.rope_bwd(*O.rope(q, k, cu, su), cu, su)
+    np.testing.assert_allclose(back[0], q, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(back[1], k, rtol=1e-12, atol=1e-12)
+
+
 # --------------------------------------------------------------------------- attention
 
 
