@@ -47,10 +47,11 @@ MEASURED_TRAFFIC: dict[str, int | None] = {
     "c1": 134_549_339,
     "c2": 1_409_309_330,
     "c3": 539_013_266,
-    "c4": 3_240_299_913,
+    "c4": 3_240_311_168,
     "c5": 2_632_999_026,
     "add_rmsnorm": 4_314_051_694,
     "rope": 337_726_126,
+    "qk_norm_rope": 510_771_483,
     "attn_bwd": 15_115_471_835,  # the dq and dk/dv kernels of one pk_attn_bwd call
     "copy": 1_073_766_308,
 }
@@ -228,6 +229,68 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                         "bf16", "TB/s", 2 * launch_bytes, step, "rope_kernel", launch_bytes, launch,
                         {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
                          "theta": 500000.0, "dtype": "bf16"}, cpu)
+
+    if name == "qk_norm_rope":
+        # not a BASELINE config: the kernel-writing notebook's fused op at its benchmark shape
+        B, HQ, HKV, S, D = 4, 32, 8, 4096, 128
+        q = _randn((B, HQ, S, D), torch.bfloat16, gen, dev)
+        k = _randn((B, HKV, S, D), torch.bfloat16, gen, dev)
+        qw, kw = _randn((D,), torch.bfloat16, gen, dev), _randn((D,), torch.bfloat16, gen, dev)
+        half = _randn((1, S, D // 2), torch.bfloat16, gen, dev)
+        cos, sin = torch.cos(half).repeat(1, 1, 2), torch.sin(half).repeat(1, 1, 2)
+        gq, gk = _randn((B, HQ, S, D), torch.bfloat16, gen, dev), _randn((B, HKV, S, D), torch.bfloat16, gen, dev)
+        qkb = (q.numel() + k.numel()) * 2
+        side = 2 * S * D * 2 + 2 * D * 2 + 4 * B * (HQ + HKV) * S  # tables, weights, rstd
+        fwd_bytes = 2 * qkb + side
+        bwd_bytes = 3 * qkb + side
+        leaves = [t.requires_grad_() for t in (q, k, qw, kw)]
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        dw = torch.empty((2, D), dtype=torch.bfloat16, device=dev)
+        rq = torch.empty((B, HQ, S), dtype=torch.float32, device=dev)
+        rk = torch.empty((B, HKV, S), dtype=torch.float32, device=dev)
+        yq, yk = torch.empty_like(q), torch.empty_like(k)
+        st12 = (_lib._i64 * 12)(*(x for t in (q, k, yq, yk) for x in t.stride()[:3]))
+        _lib.check(lib.pk_qk_norm_rope_fwd(q.data_ptr(), k.data_ptr(), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
+                                           sin.data_ptr(), yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(),
+                                           st12, B, HQ, HKV, S, D, 1, 1e-6, _lib.BF16, _lib.BF16, stream()))
+        ws_bytes = lib.pk_qk_norm_rope_bwd_workspace(B, HQ, HKV, S, D, _lib.BF16)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        st18 = (_lib._i64 * 18)(*(x for t in (q, k, gq, gk, dq, dk) for x in t.stride()[:3]))
+
+        def step(i):
+            oq, ok = impls.qk_norm_rope(*leaves, cos, sin, 1e-6)
+            torch.autograd.grad((oq, ok), leaves, (gq, gk))
+
+        def launch(i):
+            _lib.check(lib.pk_qk_norm_rope_bwd(q.data_ptr(), k.data_ptr(), qw.data_ptr(), kw.data_ptr(),
+                                               cos.data_ptr(), sin.data_ptr(), rq.data_ptr(), rk.data_ptr(),
+                                               gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                               dw.data_ptr(), ws.data_ptr(), ws_bytes, st18, B, HQ, HKV, S, D, 1,
+                                               _lib.BF16, _lib.BF16, stream()))
+
+        def cpu():
+            from popcorn_amd.compat import references as R
+
+            qc = torch.randn(1, HQ, S, D).bfloat16().requires_grad_()
+            kc = torch.randn(1, HKV, S, D).bfloat16().requires_grad_()
+            wq, wk = (torch.randn(D).bfloat16().requires_grad_() for _ in range(2))
+            cc, sc = cos.cpu(), sin.cpu()
+            gqc, gkc = torch.randn(1, HQ, S, D).bfloat16(), torch.randn(1, HKV, S, D).bfloat16()
+
+            def one():
+                oq, ok = R.qk_norm_rope(qc, kc, wq, wk, cc, sc, 1e-6)
+                torch.autograd.grad((oq, ok), (qc, kc, wq, wk), (gqc, gkc))
+
+            t, reps = _time_cpu(one)
+            qk1 = (qc.numel() + kc.numel()) * 2
+            work = 5 * qk1 + 2 * (2 * S * D * 2 + 2 * D * 2 + 4 * (HQ + HKV) * S)
+            return work / t / 1e12, f"batch 1 of {B}, fwd+bwd, median of {reps} reps"
+
+        return Workload("qk_norm_rope", "qk_norm_rope fwd+bwd bf16 q [4,32,4096,128], k [4,8,4096,128], "
+                        "weights [128], bf16 cos/sin [1,4096,128]", "bf16", "TB/s", fwd_bytes + bwd_bytes, step,
+                        "qk_norm_rope_bwd_kernel", bwd_bytes, launch,
+                        {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
+                         "eps": 1e-6, "dtype": "bf16"}, cpu)
 
     if name == "c4":
         rows, cols = 65536, 8192
@@ -493,8 +556,9 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "attn_bwd",
-                                                           "copy"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope",
+                                                           "qk_norm_rope",
+                                                           "attn_bwd", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
     args = ap.parse_args(argv)
@@ -521,7 +585,7 @@ def main(argv=None) -> int:
 
     others = {}
     if not args.no_others and wl.name != "copy":
-        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope"):
+        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope"):
             if name == wl.name:
                 continue
             del wl

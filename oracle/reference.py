@@ -31,6 +31,11 @@ independent fact that a plausible slip would break:
                     explicit per-channel loops with unequal halves
   rope_bwd          central finite differences; <rope(x), g> = <x, rope_bwd(g)>;
                     duplicated unit tables: rope_bwd inverts rope
+  qk_norm_rope      float64 torch F.rms_norm per head row then the complex rotation;
+                    eps = 0: invariant under scaling each row; unit tables and unit
+                    weights: every output row has RMS sqrt(ms / (ms + eps))
+  qk_norm_rope_bwd  central finite differences for dq, dk and both weights; float64
+                    torch autograd of F.rms_norm + rotate_half rope
   attention         explicit per-query loops; float64 SDPA with repeat_interleave;
                     q = 0 gives prefix means of v and lse = log(t + 1); S = 1 gives v
   attention_bwd     float64 torch autograd of SDPA (repeat_interleave grouping);
@@ -60,6 +65,10 @@ __all__ = [
     "attention_varlen",
     "attention_bwd",
     "attention_varlen_bwd",
+    "rope",
+    "rope_bwd",
+    "qk_norm_rope",
+    "qk_norm_rope_bwd",
 ]
 
 
@@ -187,6 +196,24 @@ def rope_bwd(dq, dk, cos, sin):
     """(dq_in, dk_in) of `rope`: the transpose g*cos + rotate_half^T(g*sin), rotate_half^T = -rotate_half."""
     c, s = _f64(cos)[:, None], _f64(sin)[:, None]
     return tuple(g * c - _rotate_half(g * s) for g in (_f64(dq), _f64(dk)))
+
+
+def qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps: float = 1e-6):
+    """RMSNorm of every q and k head row (weights over head_dim) then `rope`.
+
+    The kernel-writing notebook's reference (examples/03_write_a_kernel.ipynb,
+    cell 3): `rms(q, eps) * q_weight`, `rms(k, eps) * k_weight` (`rms`,
+    kernels/_utils.py:14-16), then kernels/rope.py:35-36.
+    """
+    return rope(rms_norm(q, q_weight, None, eps), rms_norm(k, k_weight, None, eps), cos, sin)
+
+
+def qk_norm_rope_bwd(q, k, q_weight, k_weight, cos, sin, dyq, dyk, eps: float = 1e-6):
+    """(dq, dk, dq_weight, dk_weight) of `qk_norm_rope`: rope's transpose, then the RMSNorm backward per side."""
+    gq, gk = rope_bwd(dyq, dyk, cos, sin)
+    dq, dqw, _ = rms_norm_bwd(q, q_weight, gq, eps)
+    dk, dkw, _ = rms_norm_bwd(k, k_weight, gk, eps)
+    return dq, dk, dqw, dkw
 
 
 def _rotate_half(x: np.ndarray) -> np.ndarray:

@@ -99,6 +99,33 @@ def rope_supported(q, k, cos, sin) -> bool:
     )
 
 
+def _norm_rope_head_dim(head_dim: int, dtype: torch.dtype) -> bool:
+    """head_dim / 2 = (16-byte pack) * 2^k with at most 64 packs: one row inside one wavefront."""
+    pack = 16 // torch.empty((), dtype=dtype).element_size()
+    half = head_dim // 2
+    if head_dim % 2 or half % pack:
+        return False
+    packs = half // pack
+    return 1 <= packs <= 64 and packs & (packs - 1) == 0
+
+
+def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
+    return (
+        _on_hip(q, k, q_weight, k_weight, cos, sin)
+        and q.dtype in _FLOATS
+        and q.dtype == k.dtype == q_weight.dtype == k_weight.dtype == cos.dtype == sin.dtype
+        and q.dim() == k.dim() == 4
+        and cos.dim() == 3
+        and cos.shape == sin.shape
+        and k.shape[0] == q.shape[0]
+        and k.shape[2:] == q.shape[2:]
+        and q_weight.shape == k_weight.shape == q.shape[-1:]
+        and cos.shape[1:] == q.shape[2:]
+        and cos.shape[0] in (1, q.shape[0])
+        and _norm_rope_head_dim(q.shape[-1], q.dtype)
+    )
+
+
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:
     return (
         _on_hip(q, k, v)
@@ -132,6 +159,7 @@ REGISTRATIONS = (
     ("swiglu", "popcorn_amd.impls.swiglu", swiglu_supported, False),
     ("rotary_embedding", "popcorn_amd.impls.rotary_embedding", rotary_supported, False),
     ("rope", "popcorn_amd.impls.rope", rope_supported, False),
+    ("qk_norm_rope", "popcorn_amd.impls.qk_norm_rope", qk_norm_rope_supported, False),
     ("attn", "popcorn_amd.impls.attn", attn_supported, False),
     ("attn_varlen", "popcorn_amd.impls.attn_varlen", attn_varlen_supported, False),
 )
@@ -154,7 +182,9 @@ def register(popcorn: ModuleType | None = None) -> ModuleType:
     pc = popcorn if popcorn is not None else _popcorn()
     pc.declare_backend(BACKEND, package=DISTRIBUTION, min_version=__version__, max_version=__version__)
     for op_name, source, predicate, forward_only in REGISTRATIONS:
-        op = pc.KERNELS[op_name]
+        op = pc.KERNELS.get(op_name)
+        if op is None:  # qk_norm_rope exists once defined (Popcorn's notebook does; compat ships it)
+            continue
         if BACKEND not in op.available_backends():  # registering twice is a no-op, not an error
             op.register(BACKEND, source=source, predicate=predicate, forward_only=forward_only)
     return pc

@@ -67,6 +67,27 @@ def rope(
     return references.rope(q, k, cos, sin)
 
 
+@register_kernel(test_args={"eps": [1e-6]},
+                 test_inputs={"cos": references.rope_table(torch.cos), "sin": references.rope_table(torch.sin)},
+                 tags={"normalization", "positional", "fused"})
+def qk_norm_rope(
+    q: Float[Tensor, "batch q_heads seq head_dim"],
+    k: Float[Tensor, "batch kv_heads seq head_dim"],
+    q_weight: Float[Tensor, "head_dim"],
+    k_weight: Float[Tensor, "head_dim"],
+    cos: Float[Tensor, "cos_batch seq head_dim"],
+    sin: Float[Tensor, "cos_batch seq head_dim"],
+    eps: float = 1e-6,
+) -> tuple[Tensor, Tensor]:
+    """Per-head RMS normalization of queries and keys, followed by rotary embedding.
+
+    Not an op Popcorn ships: its kernel-writing notebook defines it
+    (examples/03_write_a_kernel.ipynb, cell 3) with this signature and these
+    test inputs.
+    """
+    return references.qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps)
+
+
 @register_kernel(test_args={"softmax_scale": [None, 0.25]})
 def attn(
     q: Float[Tensor, "batch seq q_heads head_dim"],

@@ -11,6 +11,7 @@ the native-dtype rounding the budget measures:
     swiglu            kernels/swiglu.py:9-18
     rotary_embedding  kernels/rotary_embedding.py:12-40
     rope              kernels/rope.py:8-36 (`_rotate_half`, `_table`: kernels/rope.py:8-14)
+    qk_norm_rope      examples/03_write_a_kernel.ipynb, cell 3 (`rms`: kernels/_utils.py:14-16)
     attn              kernels/attn.py:10-37
     attn_varlen       kernels/attn_varlen.py:15-54 (`cuts`: kernels/_varlen.py:8-13)
 """
@@ -27,11 +28,15 @@ def upcast(t: Tensor) -> Tensor:
     return t.to(torch.promote_types(t.dtype, torch.float32))
 
 
+def rms(x: Tensor, eps: float) -> Tensor:
+    """x / sqrt(mean(x^2) + eps) over the last dimension in >= fp32, rounded to x's dtype."""
+    h = upcast(x)
+    return (h * torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)).to(x.dtype)
+
+
 def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float = 1e-6) -> Tensor:
     """Normalise in >= fp32, round to x's dtype, then scale (and shift) in that dtype."""
-    h = upcast(x)
-    inv_rms = torch.rsqrt(h.square().mean(dim=-1, keepdim=True) + eps)
-    y = (h * inv_rms).to(x.dtype) * weight
+    y = rms(x, eps) * weight
     return y if bias is None else y + bias
 
 
@@ -82,6 +87,12 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
     """
     cos, sin = cos.detach()[:, None], sin.detach()[:, None]
     return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor,
+                 eps: float = 1e-6) -> tuple[Tensor, Tensor]:
+    """`rms` of every q and k head row times its weight, then `rope`, eager at the inputs' dtype."""
+    return rope(rms(q, eps) * q_weight, rms(k, eps) * k_weight, cos, sin)
 
 
 def rope_table(f):

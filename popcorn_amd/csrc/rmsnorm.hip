@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "api.h"
+#include "colsum.h"
 #include "common.h"
 
 namespace pk {
@@ -31,7 +32,6 @@ namespace {
 
 constexpr int kThreads = 256;    // fallback kernels and column sums
 constexpr int kMaxVpt = 16;
-constexpr int kColSplit = 32;    // partial rows summed per block in the first column-sum stage
 
 // Sum over the TPR lanes that share a row: TPR = 64 is one wave; TPR = NTB is
 // the block, `red` holds one slot per wave and the call is a block barrier.
@@ -444,30 +444,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
   }
 }
 
-// Column sums of a [parts, cols] fp32 array in a fixed order. Stage one:
-// block (cx, s) sums parts [s*kColSplit, (s+1)*kColSplit) of 256 columns into
-// stage[s]; stage two sums the stage rows and rounds to T.
-__global__ __launch_bounds__(kThreads) void column_sum_stage(const float* __restrict__ part,
-                                                            float* __restrict__ stage, int64_t parts, int cols) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  const int64_t p0 = (int64_t)blockIdx.y * kColSplit;
-  const int64_t p1 = p0 + kColSplit < parts ? p0 + kColSplit : parts;
-  if (c >= cols) return;
-  float s = 0.f;
-  for (int64_t p = p0; p < p1; ++p) s += part[p * cols + c];
-  stage[(int64_t)blockIdx.y * cols + c] = s;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void column_sum_final(const float* __restrict__ stage, T* __restrict__ out,
-                                                            int64_t n, int cols) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= cols) return;
-  float s = 0.f;
-  for (int64_t p = 0; p < n; ++p) s += stage[p * cols + c];
-  out[c] = from_f32<T>(s);
-}
-
 // ---------------------------------------------------------------------------
 // launch planning
 
@@ -627,16 +603,6 @@ template <typename T, int MODE> int64_t bwd_blocks(int64_t rows, const Plan& p) 
   const int64_t want = (rows + rpb - 1) / rpb;
   const int64_t cap = (int64_t)cu_count() * per_cu;
   return want < cap ? want : cap;
-}
-
-int64_t stage_rows(int64_t parts) { return (parts + kColSplit - 1) / kColSplit; }
-
-template <typename T> void column_sums(const float* part, float* stage, T* out, int64_t parts, int cols,
-                                       hipStream_t s) {
-  const int64_t n = stage_rows(parts);
-  const int cx = (cols + kThreads - 1) / kThreads;
-  hipLaunchKernelGGL(column_sum_stage, dim3(cx, (unsigned)n), dim3(kThreads), 0, s, part, stage, parts, cols);
-  hipLaunchKernelGGL(column_sum_final<T>, dim3(cx), dim3(kThreads), 0, s, stage, out, n, cols);
 }
 
 template <typename T, int MODE> int bwd(const BwdArgs& a, const char* who) {

@@ -19,6 +19,7 @@
 // per head. Consecutive threads take consecutive chunks, then positions: a
 // wave streams contiguous rows of one head.
 #include "api.h"
+#include "colsum.h"
 #include "common.h"
 
 namespace pk {
@@ -183,6 +184,353 @@ template <typename T> int run_cs(int cs_dtype, bool vec, const void* cs, const v
   }
 }
 
+// ---------------------------------------------------------------------------
+// qk_norm_rope: per-head RMSNorm of the q and k rows (each side with its own
+// weight over head_dim), then the rotation above, in one pass:
+//
+//   r = 1 / sqrt(mean(x^2) + eps),  n = x r w,  y = n cos + rotate_half(n) sin
+//
+// and its backward, which recomputes n from x and the saved r:
+//
+//   g = rotation^T(dy),  u = g w,  dx = r (u - x r^2 <u, x> / head_dim),
+//   dw = sum over rows of g x r.
+//
+// Same tiling as rope_kernel, with two restrictions that keep every row
+// inside one wavefront: 16-byte chunks only, and chunks per row a power of
+// two up to 64, so the row's lanes are consecutive and aligned and its sums
+// are butterflies over them. A head group never mixes q and k heads, so a
+// block holds one weight vector and one dw accumulator. dw is reduced without
+// atomics: lanes of one chunk column in a wave, then the four waves through
+// LDS, into one [2 * head_dim] partial row per block (the other side's half
+// zero), summed over blocks in a fixed order by column_sums.
+
+struct NormArgs {
+  const void* x[2];   // q, k
+  void* y[2];         // forward: outputs; backward: dq, dk
+  const void* g[2];   // backward: cotangents dyq, dyk
+  const void* w[2];   // q_weight, k_weight [head_dim]
+  float* rstd[2];     // [batch, heads, seq] per side: written forward, read backward
+  int64_t xs[2][3], ys[2][3], gs[2][3];  // (batch, head, seq) strides
+  int heads[2];
+  int batch, seq, half, cos_batch;
+  int chunks, shift;  // chunks per row (a power of two) and its log2
+  int rows, tiles;    // positions per block tile, tiles per batch row
+  int group;          // heads per block
+  int groups_q;       // head groups of q; groups [groups_q, groups_q + groups_k) are k's
+  float eps, inv_d;
+  float* part;        // backward: [blocks, 2 * head_dim] partial dw rows
+};
+
+struct NormPlan {
+  int rows, tiles, group, groups_q, groups_k;
+  int64_t blocks;
+};
+
+// Head groups sized for about eight 256-thread blocks per CU, as rope_kernel.
+NormPlan norm_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int chunks) {
+  NormPlan p{};
+  p.rows = kThreads / chunks;
+  p.tiles = (int)((seq + p.rows - 1) / p.rows);
+  const int64_t all = q_heads + kv_heads;
+  const int64_t tiles = batch * p.tiles;
+  if (all == 0 || tiles == 0) return p;
+  int64_t groups = (8 * (int64_t)cu_count() + tiles - 1) / tiles;
+  groups = groups < 1 ? 1 : (groups > all ? all : groups);
+  p.group = (int)((all + groups - 1) / groups);
+  p.groups_q = (int)((q_heads + p.group - 1) / p.group);
+  p.groups_k = (int)((kv_heads + p.group - 1) / p.group);
+  p.blocks = tiles * (p.groups_q + p.groups_k);
+  return p;
+}
+
+// Sum over the `width` consecutive lanes (a power of two, aligned) that hold one row.
+__device__ __forceinline__ float row_sum(float v, int width) {
+  for (int m = 1; m < width; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+struct NormBlock {
+  int t, b, h_begin, h_end, s, j;
+};
+
+__device__ __forceinline__ NormBlock norm_block(const NormArgs& a) {
+  NormBlock nb;
+  unsigned blk = blockIdx.x;
+  const int tile = (int)(blk % (unsigned)a.tiles);
+  blk /= (unsigned)a.tiles;
+  nb.b = (int)(blk % (unsigned)a.batch);
+  int gi = (int)(blk / (unsigned)a.batch);
+  nb.t = gi >= a.groups_q;
+  if (nb.t) gi -= a.groups_q;
+  nb.h_begin = gi * a.group;
+  nb.h_end = nb.h_begin + a.group < a.heads[nb.t] ? nb.h_begin + a.group : a.heads[nb.t];
+  nb.s = tile * a.rows + (int)(threadIdx.x >> a.shift);
+  nb.j = (int)(threadIdx.x & (a.chunks - 1));
+  return nb;
+}
+
+template <typename T, typename C, int VEC, int U>
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __restrict__ cosp,
+                                                                    const C* __restrict__ sinp, NormArgs a) {
+  const NormBlock nb = norm_block(a);
+  if (nb.s >= a.seq) return;  // whole rows drop out together; no barrier below
+  const int t = nb.t, j = nb.j * VEC;
+  const int64_t hd = 2 * (int64_t)a.half;
+  const int64_t trow = ((int64_t)(a.cos_batch == 1 ? 0 : nb.b) * a.seq + nb.s) * hd + j;
+  float c1[VEC], c2[VEC], s1[VEC], s2[VEC], w1[VEC], w2[VEC];
+  table(cosp + trow, c1);
+  table(cosp + trow + a.half, c2);
+  table(sinp + trow, s1);
+  table(sinp + trow + a.half, s2);
+  const T* wp = static_cast<const T*>(a.w[t]);
+  table(wp + j, w1);
+  table(wp + a.half + j, w2);
+  const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
+  T* yb = static_cast<T*>(a.y[t]) + nb.b * a.ys[t][0] + nb.s * a.ys[t][2] + j;
+  float* rb = a.rstd[t] + ((int64_t)nb.b * a.heads[t]) * a.seq + nb.s;
+  for (int h0 = nb.h_begin; h0 < nb.h_end; h0 += U) {
+    Pack<T, VEC> x1[U], x2[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (h0 + u >= nb.h_end) break;
+      const T* xr = xb + (h0 + u) * a.xs[t][1];
+      x1[u].load(xr);
+      x2[u].load(xr + a.half);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (h0 + u >= nb.h_end) break;
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float p = to_f32(x1[u].v[k]), q = to_f32(x2[u].v[k]);
+        ss += p * p + q * q;
+      }
+      const float r = rsqrtf(row_sum(ss, a.chunks) * a.inv_d + a.eps);
+      Pack<T, VEC> y1, y2;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float n1 = to_f32(x1[u].v[k]) * r * w1[k], n2 = to_f32(x2[u].v[k]) * r * w2[k];
+        y1.v[k] = from_f32<T>(n1 * c1[k] - n2 * s1[k]);
+        y2.v[k] = from_f32<T>(n2 * c2[k] + n1 * s2[k]);
+      }
+      T* yr = yb + (h0 + u) * a.ys[t][1];
+      y1.store(yr);
+      y2.store(yr + a.half);
+      if (nb.j == 0) rb[(int64_t)(h0 + u) * a.seq] = r;
+    }
+  }
+}
+
+template <typename T, typename C, int VEC, int U>
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_bwd_kernel(const C* __restrict__ cosp,
+                                                                    const C* __restrict__ sinp, NormArgs a) {
+  extern __shared__ float red[];  // [4 waves][2 * half]
+  const NormBlock nb = norm_block(a);
+  const int t = nb.t, j = nb.j * VEC;
+  float dw1[VEC], dw2[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) dw1[k] = dw2[k] = 0.f;
+  if (nb.s < a.seq) {  // rows past the end keep zero partials but join the reduction
+    const int64_t hd = 2 * (int64_t)a.half;
+    const int64_t trow = ((int64_t)(a.cos_batch == 1 ? 0 : nb.b) * a.seq + nb.s) * hd + j;
+    float c1[VEC], c2[VEC], s1[VEC], s2[VEC], w1[VEC], w2[VEC];
+    table(cosp + trow, c1);
+    table(cosp + trow + a.half, c2);
+    table(sinp + trow, s1);
+    table(sinp + trow + a.half, s2);
+    const T* wp = static_cast<const T*>(a.w[t]);
+    table(wp + j, w1);
+    table(wp + a.half + j, w2);
+    const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
+    const T* gb = static_cast<const T*>(a.g[t]) + nb.b * a.gs[t][0] + nb.s * a.gs[t][2] + j;
+    T* db = static_cast<T*>(a.y[t]) + nb.b * a.ys[t][0] + nb.s * a.ys[t][2] + j;
+    const float* rb = a.rstd[t] + ((int64_t)nb.b * a.heads[t]) * a.seq + nb.s;
+    for (int h0 = nb.h_begin; h0 < nb.h_end; h0 += U) {
+      Pack<T, VEC> x1[U], x2[U], g1[U], g2[U];
+      float r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (h0 + u >= nb.h_end) break;
+        const T* xr = xb + (h0 + u) * a.xs[t][1];
+        const T* gr = gb + (h0 + u) * a.gs[t][1];
+        x1[u].load(xr);
+        x2[u].load(xr + a.half);
+        g1[u].load(gr);
+        g2[u].load(gr + a.half);
+        r[u] = rb[(int64_t)(h0 + u) * a.seq];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (h0 + u >= nb.h_end) break;
+        float e1[VEC], e2[VEC], u1[VEC], u2[VEC];
+        float dot = 0.f;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const float d1 = to_f32(g1[u].v[k]), d2 = to_f32(g2[u].v[k]);
+          e1[k] = d1 * c1[k] + d2 * s2[k];  // gradient reaching n (transposed rotation)
+          e2[k] = d2 * c2[k] - d1 * s1[k];
+          u1[k] = e1[k] * w1[k];
+          u2[k] = e2[k] * w2[k];
+          dot += u1[k] * to_f32(x1[u].v[k]) + u2[k] * to_f32(x2[u].v[k]);
+        }
+        const float rr = r[u];
+        const float coef = rr * rr * row_sum(dot, a.chunks) * a.inv_d;
+        Pack<T, VEC> o1, o2;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const float p = to_f32(x1[u].v[k]), q = to_f32(x2[u].v[k]);
+          o1.v[k] = from_f32<T>(rr * (u1[k] - p * coef));
+          o2.v[k] = from_f32<T>(rr * (u2[k] - q * coef));
+          dw1[k] += e1[k] * p * rr;
+          dw2[k] += e2[k] * q * rr;
+        }
+        T* dr = db + (h0 + u) * a.ys[t][1];
+        o1.store(dr);
+        o2.store(dr + a.half);
+      }
+    }
+  }
+  // dw: lanes of one chunk column within the wave, then the four waves
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    for (int m = a.chunks; m < 64; m <<= 1) {
+      dw1[k] += __shfl_xor(dw1[k], m, 64);
+      dw2[k] += __shfl_xor(dw2[k], m, 64);
+    }
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int hd = 2 * a.half;
+  if (lane < a.chunks) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      red[wave * hd + j + k] = dw1[k];
+      red[wave * hd + a.half + j + k] = dw2[k];
+    }
+  }
+  __syncthreads();
+  float* out = a.part + (int64_t)blockIdx.x * 2 * hd;
+  for (int c = threadIdx.x; c < 2 * hd; c += kThreads) {
+    const int side = c >= hd, col = c - side * hd;
+    float v = 0.f;
+    if (side == t) v = ((red[col] + red[hd + col]) + red[2 * hd + col]) + red[3 * hd + col];
+    out[c] = v;
+  }
+}
+
+// 16-byte chunks with a power-of-two count per row, at most 64; 0 when unsupported.
+int norm_chunks(int64_t head_dim, int x_dtype) {
+  const int64_t V = 16 / elem_size(x_dtype);
+  const int64_t half = head_dim / 2;
+  if (head_dim % 2 != 0 || half % V != 0) return 0;
+  const int64_t c = half / V;
+  return (c >= 1 && c <= 64 && (c & (c - 1)) == 0) ? (int)c : 0;
+}
+
+int64_t norm_workspace(const NormPlan& p, int64_t head_dim) {
+  auto up = [](int64_t n) { return (n + 255) / 256 * 256; };
+  const int64_t cols = 2 * head_dim;
+  return up(p.blocks * cols * (int64_t)sizeof(float)) + up(stage_rows(p.blocks) * cols * (int64_t)sizeof(float));
+}
+
+template <typename T, typename C>
+int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const NormPlan& p, void* dw, void* ws,
+                hipStream_t s) {
+  constexpr int VEC = 16 / sizeof(T);
+  const C* c = static_cast<const C*>(cs);
+  const C* n = static_cast<const C*>(sn);
+  if (!backward) {
+    if (p.blocks > 0)
+      hipLaunchKernelGGL((qk_norm_rope_fwd_kernel<T, C, VEC, 4>), dim3((unsigned)p.blocks), dim3(kThreads), 0, s, c,
+                         n, a);
+    return launched("pk_qk_norm_rope_fwd");
+  }
+  const int cols = 4 * a.half;
+  auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+  a.part = static_cast<float*>(ws);
+  float* stage = reinterpret_cast<float*>(static_cast<char*>(ws) + up(p.blocks * cols * (int64_t)sizeof(float)));
+  if (p.blocks > 0) {
+    const size_t lds = 4 * (size_t)(2 * a.half) * sizeof(float);
+    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, C, VEC, 2>), dim3((unsigned)p.blocks), dim3(kThreads), lds, s, c,
+                       n, a);
+    column_sums<T>(a.part, stage, static_cast<T*>(dw), p.blocks, cols, s);
+  } else {  // nothing to sum: dw is zero
+    hipLaunchKernelGGL(column_sum_final<T>, dim3((cols + kFinalCols - 1) / kFinalCols), dim3(kColThreads), 0, s,
+                       stage, static_cast<T*>(dw), (int64_t)0, cols);
+  }
+  return launched("pk_qk_norm_rope_bwd");
+}
+
+// Shared validation and argument set-up of the two entry points.
+int norm_setup(const char* who, NormArgs& a, NormPlan& p, const void* q, const void* k, const void* qw,
+               const void* kw, const void* cos, const void* sin, const int64_t* strides, int nstrides, int64_t batch,
+               int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim, int64_t cos_batch, int x_dtype,
+               int cs_dtype) {
+  if (batch < 0 || q_heads < 0 || kv_heads < 0 || seq < 0 || head_dim < 0)
+    return fail(PK_ERR_INVALID, "%s: negative size", who);
+  if (cos_batch != 1 && cos_batch != batch)
+    return fail(PK_ERR_INVALID, "%s: cos_batch=%lld is neither 1 nor batch=%lld", who, (long long)cos_batch,
+                (long long)batch);
+  if (!known_dtype(x_dtype) || !known_dtype(cs_dtype))
+    return fail(PK_ERR_UNSUPPORTED, "%s: dtype codes %d/%d", who, x_dtype, cs_dtype);
+  if (batch > INT32_MAX || seq > INT32_MAX || q_heads + kv_heads > INT32_MAX || head_dim > INT32_MAX)
+    return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
+  const int chunks = norm_chunks(head_dim, x_dtype);
+  if (head_dim > 0 && chunks == 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld is not 2 * (16-byte packs) * 2^k with at most 64 packs", who,
+                (long long)head_dim);
+  a = NormArgs{};
+  a.chunks = chunks > 0 ? chunks : 1;
+  while ((1 << a.shift) < a.chunks) ++a.shift;
+  p = norm_plan(batch, q_heads, kv_heads, seq, a.chunks);
+  if (p.blocks > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: %lld blocks exceed the grid", who, (long long)p.blocks);
+  a.heads[0] = (int)q_heads;
+  a.heads[1] = (int)kv_heads;
+  a.batch = (int)batch;
+  a.seq = (int)seq;
+  a.half = (int)(head_dim / 2);
+  a.cos_batch = (int)cos_batch;
+  a.rows = p.rows;
+  a.tiles = p.tiles;
+  a.group = p.group;
+  a.groups_q = p.groups_q;
+  a.inv_d = head_dim > 0 ? 1.0f / (float)head_dim : 0.f;
+  if (p.blocks == 0) return PK_OK;  // nothing to read (a backward still zeroes dw)
+  if (!cos || !sin || !strides || (q_heads > 0 && (!q || !qw)) || (kv_heads > 0 && (!k || !kw)))
+    return fail(PK_ERR_INVALID, "%s: null pointer", who);
+  const void* ptrs[] = {q, k, qw, kw};
+  for (const void* ptr : ptrs)
+    if (ptr && !aligned16(ptr)) return fail(PK_ERR_UNSUPPORTED, "%s: q, k and the weights must be 16-byte aligned", who);
+  if ((16 / elem_size(x_dtype) * elem_size(cs_dtype)) % 16 == 0 && !(aligned16(cos) && aligned16(sin)))
+    return fail(PK_ERR_UNSUPPORTED, "%s: cos and sin must be 16-byte aligned", who);
+  const int64_t V = 16 / elem_size(x_dtype);
+  for (int i = 0; i < nstrides; ++i)
+    if (strides[i] % V != 0) return fail(PK_ERR_UNSUPPORTED, "%s: strides must be multiples of %lld", who, (long long)V);
+  a.x[0] = q;
+  a.x[1] = k;
+  a.w[0] = qw;
+  a.w[1] = kw;
+  return PK_OK;
+}
+
+template <typename T> int norm_run_cs(int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
+                                      const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+  switch (cs_dtype) {
+    case PK_F32: return norm_launch<T, float>(backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_launch<T, bf16>(backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_launch<T, f16>(backward, cs, sn, a, p, dw, ws, s);
+  }
+}
+
+int norm_run(int x_dtype, int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
+             const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+  switch (x_dtype) {
+    case PK_F32: return norm_run_cs<float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_run_cs<bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_run_cs<f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+  }
+}
+
 }  // namespace
 }  // namespace pk
 
@@ -239,6 +587,84 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
     case PK_BF16: return run_cs<bf16>(cs_dtype, vec, cos, sin, a, transpose, s);
     default: return run_cs<f16>(cs_dtype, vec, cos, sin, a, transpose, s);
   }
+}
+
+int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
+                        const void* sin, void* yq, void* yk, float* rstd_q, float* rstd_k, const int64_t* strides,
+                        int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+                        int64_t cos_batch, float eps, int x_dtype, int cs_dtype, void* stream) {
+  using namespace pk;
+  NormArgs a;
+  NormPlan p;
+  int rc = norm_setup("pk_qk_norm_rope_fwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 12, batch, q_heads,
+                      kv_heads, seq, head_dim, cos_batch, x_dtype, cs_dtype);
+  if (rc != PK_OK || p.blocks == 0) return rc;
+  if ((q_heads > 0 && (!yq || !rstd_q)) || (kv_heads > 0 && (!yk || !rstd_k)))
+    return fail(PK_ERR_INVALID, "pk_qk_norm_rope_fwd: null output");
+  if ((yq && !aligned16(yq)) || (yk && !aligned16(yk)))
+    return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_fwd: outputs must be 16-byte aligned");
+  a.y[0] = yq;
+  a.y[1] = yk;
+  a.rstd[0] = rstd_q;
+  a.rstd[1] = rstd_k;
+  for (int i = 0; i < 3; ++i) {
+    a.xs[0][i] = strides[i];
+    a.xs[1][i] = strides[3 + i];
+    a.ys[0][i] = strides[6 + i];
+    a.ys[1][i] = strides[9 + i];
+  }
+  a.eps = eps;
+  return norm_run(x_dtype, cs_dtype, false, cos, sin, a, p, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
+                                      int64_t head_dim, int x_dtype) {
+  using namespace pk;
+  if (batch < 0 || q_heads < 0 || kv_heads < 0 || seq < 0 || head_dim < 0 || !known_dtype(x_dtype)) return -1;
+  const int chunks = norm_chunks(head_dim, x_dtype);
+  if (head_dim > 0 && chunks == 0) return -1;
+  const NormPlan p = norm_plan(batch, q_heads, kv_heads, seq, chunks > 0 ? chunks : 1);
+  return norm_workspace(p, head_dim);
+}
+
+int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
+                        const void* sin, const float* rstd_q, const float* rstd_k, const void* dyq, const void* dyk,
+                        void* dq, void* dk, void* dw, void* workspace, int64_t workspace_bytes,
+                        const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
+                        int64_t head_dim, int64_t cos_batch, int x_dtype, int cs_dtype, void* stream) {
+  using namespace pk;
+  NormArgs a;
+  NormPlan p;
+  int rc = norm_setup("pk_qk_norm_rope_bwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 18, batch, q_heads,
+                      kv_heads, seq, head_dim, cos_batch, x_dtype, cs_dtype);
+  if (rc != PK_OK || head_dim == 0) return rc;
+  if (!dw) return fail(PK_ERR_INVALID, "pk_qk_norm_rope_bwd: null dw");
+  const int64_t need = norm_workspace(p, head_dim);
+  if ((need > 0 && !workspace) || workspace_bytes < need)
+    return fail(PK_ERR_INVALID, "pk_qk_norm_rope_bwd: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  if (p.blocks > 0) {
+    if ((q_heads > 0 && (!dyq || !dq || !rstd_q)) || (kv_heads > 0 && (!dyk || !dk || !rstd_k)))
+      return fail(PK_ERR_INVALID, "pk_qk_norm_rope_bwd: null pointer");
+    const void* outs[] = {dyq, dyk, dq, dk};
+    for (const void* ptr : outs)
+      if (ptr && !aligned16(ptr)) return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_bwd: 16-byte alignment required");
+    a.g[0] = dyq;
+    a.g[1] = dyk;
+    a.y[0] = dq;
+    a.y[1] = dk;
+    a.rstd[0] = const_cast<float*>(rstd_q);
+    a.rstd[1] = const_cast<float*>(rstd_k);
+    for (int i = 0; i < 3; ++i) {
+      a.xs[0][i] = strides[i];
+      a.xs[1][i] = strides[3 + i];
+      a.gs[0][i] = strides[6 + i];
+      a.gs[1][i] = strides[9 + i];
+      a.ys[0][i] = strides[12 + i];
+      a.ys[1][i] = strides[15 + i];
+    }
+  }
+  return norm_run(x_dtype, cs_dtype, true, cos, sin, a, p, dw, workspace, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -12,6 +12,8 @@ host-side or torch fallback: an input the kernels do not cover raises.
     swiglu(a, b)                                    kernels/swiglu.py:9-18
     rotary_embedding(x, cos, sin, interleaved=False) kernels/rotary_embedding.py:12-40
     rope(q, k, cos, sin)                            kernels/rope.py:19-36
+    qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps=1e-6)
+                                                    examples/03_write_a_kernel.ipynb, cell 3
     attn(q, k, v, causal=False, softmax_scale=None) kernels/attn.py:10-37
     attn_varlen(q, k, v, cu_seqlens, causal=False, softmax_scale=None)
                                                     kernels/attn_varlen.py:15-54
@@ -25,7 +27,8 @@ from torch import Tensor
 from popcorn_amd import _lib
 
 __all__ = ["rms_norm", "add_rms_norm", "swiglu", "rotary_embedding", "attn", "attn_with_lse", "attn_varlen",
-           "attn_varlen_with_lse", "rotary_embedding_", "rope"]
+           "attn_varlen_with_lse", "rotary_embedding_", "rope",
+           "qk_norm_rope"]
 
 
 def _require_cuda(*tensors: Tensor | None) -> torch.device:
@@ -395,6 +398,91 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
     return _Rope.apply(q, k, cos, sin)
 
 
+def _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin):
+    device = _require_cuda(q, k, q_weight, k_weight, cos, sin)
+    dtype = _same_dtype("qk_norm_rope", q, k, q_weight, k_weight, cos, sin)
+    if q.dim() != 4 or k.dim() != 4 or cos.dim() != 3 or cos.shape != sin.shape:
+        raise ValueError("popcorn_amd.qk_norm_rope: q [b, hq, s, d], k [b, hkv, s, d], cos, sin [cb, s, d] expected")
+    batch, _, seq, head_dim = q.shape
+    if k.shape[0] != batch or k.shape[2:] != q.shape[2:]:
+        raise ValueError(f"popcorn_amd.qk_norm_rope: q {tuple(q.shape)} and k {tuple(k.shape)} disagree")
+    if q_weight.shape != (head_dim,) or k_weight.shape != (head_dim,):
+        raise ValueError(f"popcorn_amd.qk_norm_rope: weights must be [{head_dim}]")
+    if cos.shape[1:] != (seq, head_dim) or cos.shape[0] not in (1, batch):
+        raise ValueError(f"popcorn_amd.qk_norm_rope: cos/sin {tuple(cos.shape)} must be [1 or {batch}, {seq}, {head_dim}]")
+    return device, dtype, batch, seq, head_dim
+
+
+def _dense(t: Tensor) -> Tensor:
+    """Contiguous and 16-byte aligned (weights and tables)."""
+    c = t.detach().contiguous()
+    return c if c.data_ptr() % 16 == 0 else c.clone()
+
+
+class _QkNormRope(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, q_weight, k_weight, cos, sin, eps):
+        device, dtype, batch, seq, head_dim = _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin)
+        q_, k_ = _aligned_rows(q.detach()), _aligned_rows(k.detach())
+        qw, kw, cs, sn = (_dense(t) for t in (q_weight, k_weight, cos, sin))
+        yq, yk = torch.empty(q.shape, dtype=dtype, device=device), torch.empty(k.shape, dtype=dtype, device=device)
+        rq = torch.empty((batch, q.shape[1], seq), dtype=torch.float32, device=device)
+        rk = torch.empty((batch, k.shape[1], seq), dtype=torch.float32, device=device)
+        lib = _lib.load()
+        st = (_lib._i64 * 12)(*(x for t in (q_, k_, yq, yk) for x in t.stride()[:3]))
+        code = _lib.dtype_code(dtype)
+        _lib.check(
+            lib.pk_qk_norm_rope_fwd(
+                q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
+                yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
+                head_dim, cos.shape[0], float(eps), code, code, _lib.stream_handle(device),
+            ),
+            lib,
+        )
+        ctx.save_for_backward(q_, k_, qw, kw, cs, sn, rq, rk)
+        return yq, yk
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        q_, k_, qw, kw, cs, sn, rq, rk = ctx.saved_tensors
+        batch, _, seq, head_dim = q_.shape
+        gq = torch.zeros_like(q_) if gq is None else _aligned_rows(gq.to(q_.dtype))
+        gk = torch.zeros_like(k_) if gk is None else _aligned_rows(gk.to(k_.dtype))
+        dq, dk = torch.empty(q_.shape, dtype=q_.dtype, device=q_.device), torch.empty(k_.shape, dtype=k_.dtype,
+                                                                                       device=k_.device)
+        dw = torch.empty((2, head_dim), dtype=q_.dtype, device=q_.device)
+        lib = _lib.load()
+        code = _lib.dtype_code(q_.dtype)
+        nbytes = lib.pk_qk_norm_rope_bwd_workspace(batch, q_.shape[1], k_.shape[1], seq, head_dim, code)
+        if nbytes < 0:
+            raise ValueError(f"popcorn_amd.qk_norm_rope: head_dim={head_dim} is not supported")
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q_.device)
+        st = (_lib._i64 * 18)(*(x for t in (q_, k_, gq, gk, dq, dk) for x in t.stride()[:3]))
+        _lib.check(
+            lib.pk_qk_norm_rope_bwd(
+                q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
+                rq.data_ptr(), rk.data_ptr(), gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                dw.data_ptr(), ws.data_ptr(), nbytes, st, batch, q_.shape[1], k_.shape[1], seq, head_dim,
+                cs.shape[0], code, code, _lib.stream_handle(q_.device),
+            ),
+            lib,
+        )
+        return dq, dk, dw[0], dw[1], None, None, None
+
+
+def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor,
+                 eps: float = 1e-6) -> tuple[Tensor, Tensor]:
+    """Per-head RMSNorm of q and k (weights over head_dim), then `rope`, fused into one pass.
+
+    q [batch, q_heads, seq, head_dim], k [batch, kv_heads, seq, head_dim],
+    q_weight, k_weight [head_dim], cos, sin [cos_batch, seq, head_dim], all one
+    dtype; head_dim / 2 a 16-byte pack count times a power of two up to 64.
+    fp32 arithmetic, one rounding per output. Backward gives dq, dk and the
+    two weight gradients; cos and sin get none.
+    """
+    return _QkNormRope.apply(q, k, q_weight, k_weight, cos, sin, eps)
+
+
 # --------------------------------------------------------------------------- attention
 
 
@@ -479,7 +567,10 @@ class _Attention(torch.autograd.Function):
 def _aligned_rows(t: Tensor) -> Tensor:
     """A view the kernel can read with 16-byte loads, copying only when it must."""
     ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 and s >= 0 for s in t.stride()[:-1])
-    return t if ok else t.contiguous()
+    if ok:
+        return t
+    c = t.contiguous()
+    return c if c.data_ptr() % 16 == 0 else c.clone()  # a contiguous view at an odd offset
 
 
 def attn_varlen_with_lse(

@@ -109,6 +109,17 @@ def test_rope_records_and_routes_with_grad():
     _check_record_and_route(op, record, lambda: op(q, k, cos, sin))
 
 
+def test_qk_norm_rope_records_and_routes_with_grad():
+    op = compat.KERNELS["qk_norm_rope"]
+    q, k = _randn(4, 32, 1024, 128).requires_grad_(), _randn(4, 8, 1024, 128, seed=1).requires_grad_()
+    qw, kw = _randn(128, seed=3).requires_grad_(), _randn(128, seed=4).requires_grad_()
+    ang = _randn(1, 1024, 64, dtype=torch.float32, seed=2)
+    cos, sin = (f(ang).repeat(1, 1, 2).bfloat16() for f in (torch.cos, torch.sin))
+    [record] = op.benchmark(q, k, qw, kw, cos, sin, 1e-6, backend=NAME)
+    assert record.result.grad and {"q", "k", "q_weight", "k_weight"} <= set(record.result.bwd)
+    _check_record_and_route(op, record, lambda: op(q, k, qw, kw, cos, sin, 1e-6))
+
+
 def test_attn_records_and_routes_with_grad():
     op = compat.KERNELS["attn"]
     q, k, v = _randn(1, 1024, 8, 128), _randn(1, 1024, 2, 128, seed=1), _randn(1, 1024, 2, 128, seed=2)

@@ -326,6 +326,69 @@ def test_rope_bwd_is_the_adjoint():
     np.testing.assert_allclose(back[1], k, rtol=1e-12, atol=1e-12)
 
 
+def _qknr_torch64(q, k, qw, kw, c, s, eps):
+    """float64 torch: F.rms_norm over head rows, then y = n*cos + rotate_half(n)*sin."""
+    out = []
+    for x, w in ((q, qw), (k, kw)):
+        n = torch.nn.functional.rms_norm(torch.from_numpy(x), (x.shape[-1],), torch.from_numpy(w), eps)
+        h = x.shape[-1] // 2
+        rot = torch.cat((-n[..., h:], n[..., :h]), -1)
+        out.append(n * torch.from_numpy(c)[:, None] + rot * torch.from_numpy(s)[:, None])
+    return out
+
+
+def test_qk_norm_rope_matches_float64_torch_and_its_invariants():
+    r = rng(19)
+    b, hq, hkv, seq, d = 2, 4, 2, 5, 16
+    q, k = r.standard_normal((b, hq, seq, d)), r.standard_normal((b, hkv, seq, d))
+    qw, kw = r.standard_normal(d), r.standard_normal(d)
+    for cb in (1, b):
+        c, s = r.standard_normal((cb, seq, d)), r.standard_normal((cb, seq, d))
+        for got, want in zip(O.qk_norm_rope(q, k, qw, kw, c, s, 1e-5), _qknr_torch64(q, k, qw, kw, c, s, 1e-5)):
+            np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-12)
+    # eps = 0: each head row may be scaled by any positive factor
+    c, s = r.standard_normal((1, seq, d)), r.standard_normal((1, seq, d))
+    scale = np.exp(r.standard_normal((b, hq, seq, 1)))
+    a1 = O.qk_norm_rope(q, k, qw, kw, c, s, 0.0)[0]
+    a2 = O.qk_norm_rope(q * scale, k, qw, kw, c, s, 0.0)[0]
+    np.testing.assert_allclose(a1, a2, rtol=1e-12, atol=1e-12)
+    # unit weights, rotation tables: row RMS is sqrt(ms / (ms + eps))
+    cu, su = _tables(seq, d // 2)
+    cu, su = _dup(cu)[None], _dup(su)[None]
+    eps = 0.3
+    y = O.qk_norm_rope(q, k, np.ones(d), np.ones(d), cu, su, eps)[0]
+    ms = np.mean(q * q, axis=-1)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), np.sqrt(ms / (ms + eps)), rtol=1e-12)
+
+
+def test_qk_norm_rope_bwd_by_finite_differences_and_autograd():
+    r = rng(20)
+    b, hq, hkv, seq, d = 1, 2, 1, 3, 8
+    q, k = r.standard_normal((b, hq, seq, d)), r.standard_normal((b, hkv, seq, d))
+    qw, kw = r.standard_normal(d), r.standard_normal(d)
+    c, s = r.standard_normal((1, seq, d)), r.standard_normal((1, seq, d))
+    gq, gk = r.standard_normal(q.shape), r.standard_normal(k.shape)
+    eps = 1e-3
+    dq, dk, dqw, dkw = O.qk_norm_rope_bwd(q, k, qw, kw, c, s, gq, gk, eps)
+
+    def loss():
+        yq, yk = O.qk_norm_rope(q, k, qw, kw, c, s, eps)
+        return float(np.sum(yq * gq) + np.sum(yk * gk))
+
+    for got, x in ((dq, q), (dk, k), (dqw, qw), (dkw, kw)):
+        np.testing.assert_allclose(got, _finite_diff(loss, x), rtol=1e-6, atol=1e-7)
+    leaves = [torch.from_numpy(t.copy()).requires_grad_() for t in (q, k, qw, kw)]
+    tq, tk, tqw, tkw = leaves
+    outs = []
+    for x, w in ((tq, tqw), (tk, tkw)):
+        n = torch.nn.functional.rms_norm(x, (d,), w, eps)
+        rot = torch.cat((-n[..., d // 2:], n[..., : d // 2]), -1)
+        outs.append(n * torch.from_numpy(c)[:, None] + rot * torch.from_numpy(s)[:, None])
+    grads = torch.autograd.grad(outs, leaves, [torch.from_numpy(gq), torch.from_numpy(gk)])
+    for got, want in zip((dq, dk, dqw, dkw), grads):
+        np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-12)
+
+
 # --------------------------------------------------------------------------- attention
 
 
