@@ -4,8 +4,13 @@ Behaviour follows bench/store.py:
   * the user cache is `$POPCORN_CACHE_DIR` (else `$XDG_CACHE_HOME/popcorn`,
     else `~/.cache/popcorn`) + `/v3/reports/<op>.jsonl` (:62-72);
   * bundled rows live in `<op>.parquet` or `<op>.jsonl` of a reports
-    directory (:149-153); Parquet rows carry config/fwd/bwd/bench as JSON text
-    columns (:31-57, 116-133);
+    directory (:149-153); Parquet files have the stated 21-column schema, with
+    config/fwd/bwd/bench as JSON text (sorted keys) and zstd compression
+    (:31-57, 116-133), so files written here and Popcorn's load in either;
+  * `read(directory)` returns every row of a reports directory (:148-151),
+    `scrub` rewrites it without selected rows (:382-409), and `publish` upserts
+    the user cache's rows into `<op>.parquet` files, the offline half of
+    Popcorn's publish step (bench/__main__.py:305-308);
   * `write` upserts by `Record.key` under a process lock plus `flock`, via a
     temporary file and `os.replace` (:102-113, 358-379);
   * `merged(op)` overlays bundled and user rows by key minus the op name,
@@ -115,7 +120,7 @@ def write_parquet(records: Iterable[Record], path: Path) -> None:
         for name in NESTED:
             row[name] = json.dumps(row.get(name) or {}, sort_keys=True)
         rows.append(row)
-    pq.write_table(pa.Table.from_pylist(rows, schema=_parquet_schema()), path)
+    pq.write_table(pa.Table.from_pylist(rows, schema=_parquet_schema()), path, compression="zstd")
 
 
 def read_file(path: Path | str) -> list[Record]:
@@ -126,6 +131,13 @@ def read_file(path: Path | str) -> list[Record]:
         return [Record.from_dict(json.loads(line)) for line in path.read_text().splitlines() if line.strip()]
     except FileNotFoundError:
         return []
+
+
+def read(directory: Path | str) -> list[Record]:
+    """Every row of a reports directory: its Parquet files, then its JSONL files, each in name order."""
+    directory = Path(directory)
+    paths = sorted(directory.glob(f"*{PUBLISHED}")) + sorted(directory.glob(f"*{SCRATCH}"))
+    return [record for path in paths for record in read_file(path)]
 
 
 def bundled_path(directory: Path, op: str) -> Path:
@@ -161,6 +173,45 @@ def write(records: Iterable[Record], directory: Path | str, suffix: str = SCRATC
                 os.replace(tmp, path)
             finally:
                 tmp.unlink(missing_ok=True)
+
+
+def scrub(directory: Path | str, drop) -> int:
+    """Rewrite a reports directory without the rows `drop(record)` selects; files left empty are
+    removed. Returns the number of rows dropped."""
+    directory = Path(directory)
+    dropped = 0
+    for path in sorted(directory.glob(f"*{PUBLISHED}")) + sorted(directory.glob(f"*{SCRATCH}")):
+        with _locked(path):
+            rows = read_file(path)
+            kept = [r for r in rows if not drop(r)]
+            if len(kept) == len(rows):
+                continue
+            dropped += len(rows) - len(kept)
+            if not kept:
+                path.unlink()
+                continue
+            tmp = path.with_name(f".{path.name}.{os.getpid()}.tmp")
+            try:
+                _dump(kept, tmp, path.suffix)
+                os.replace(tmp, path)
+            finally:
+                tmp.unlink(missing_ok=True)
+    return dropped
+
+
+def publish(directory: Path | str, ops: Iterable[str] | None = None, user: Path | str | None = None) -> int:
+    """Upsert the user cache's rows (all ops, or those named) into `<directory>/<op>.parquet`.
+
+    The result is a reports directory in Popcorn's published format: rows from
+    this device merge into it by key exactly as Popcorn's own writes do.
+    Returns the number of rows offered.
+    """
+    source = Path(user) if user is not None else user_reports()
+    wanted = None if ops is None else set(ops)
+    rows = [r for path in sorted(source.glob(f"*{SCRATCH}")) for r in read_file(path)
+            if wanted is None or r.op in wanted]
+    write(rows, directory, PUBLISHED)
+    return len(rows)
 
 
 class Store:

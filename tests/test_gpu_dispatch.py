@@ -120,6 +120,17 @@ def test_qk_norm_rope_records_and_routes_with_grad():
     _check_record_and_route(op, record, lambda: op(q, k, qw, kw, cos, sin, 1e-6))
 
 
+def test_recorded_rows_publish_to_popcorns_parquet_layout(tmp_path):
+    """Rows this device records load back from `<op>.parquet` unchanged, ready to merge into Popcorn's reports."""
+    op = compat.KERNELS["swiglu"]
+    a, b = _randn(2048, 4096).requires_grad_(), _randn(2048, 4096, seed=1).requires_grad_()
+    [record] = op.benchmark(a, b, backend=NAME)
+    assert store.publish(tmp_path, ops=["swiglu"]) >= 1
+    back = store.read_file(tmp_path / "swiglu.parquet")
+    assert any(r.to_dict() == record.to_dict() for r in back)
+    assert {r.environment.device for r in back} == {torch.cuda.get_device_name()}
+
+
 def test_attn_records_and_routes_with_grad():
     op = compat.KERNELS["attn"]
     q, k, v = _randn(1, 1024, 8, 128), _randn(1, 1024, 2, 128, seed=1), _randn(1, 1024, 2, 128, seed=2)
