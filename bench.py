@@ -48,7 +48,7 @@ MEASURED_TRAFFIC: dict[str, int | None] = {
     "c2": 1_409_309_330,
     "c3": 539_013_266,
     "c4": 3_240_311_168,
-    "c5": 2_632_999_026,
+    "c5": 1_473_428_267,
     "add_rmsnorm": 4_314_051_694,
     "rope": 337_726_126,
     "qk_norm_rope": 510_771_483,

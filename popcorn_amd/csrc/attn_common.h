@@ -37,6 +37,16 @@ __device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, int voffset, i
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16 bytes at voffset + soffset of a buffer resource written straight to LDS:
+// lane i's bytes land at lds + 16 * i (lds must be the same for the whole
+// wave); zeros past the resource's range. Completion is counted by vmcnt.
+__device__ __forceinline__ void ld_buf_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
+}
+
+// Wait until this wave's LDS-bound buffer loads have landed.
+__device__ __forceinline__ void lds_loads_landed() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Four 16-bit values as two packed 32-bit words
 template <typename T> __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
   return make_uint2((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(a)) |

@@ -20,9 +20,12 @@
 // Software pipeline (per wave): step t masks S(t), exponentiates it and
 // multiplies P(t) into O while the matrix cores compute S(t+1) from the
 // next K tile, so the softmax arithmetic of one tile overlaps the matrix
-// work of the next. Staging runs ahead of that: the step issues the global
-// loads of K(t+2) and V(t+1) and stores them to LDS at its end, into
-// buffers every wave has finished with; one barrier per step.
+// work of the next. Staging runs ahead of that: the step starts by issuing
+// K(t+2) and V(t+1) as buffer loads that write LDS directly (no staging
+// registers, no LDS stores), into buffers every wave has finished with, and
+// ends once they have landed; one barrier per step. Without staging
+// registers the head_dim-128 kernel fits three waves per SIMD (three blocks
+// per CU).
 //
 // Softmax with a fixed reference max: m is the row max of s * c over the
 // first key tile (key 0 is visible to every row) and stays put, so no step
@@ -36,7 +39,9 @@
 // when the max grows by more than 2^8), so the result never depends on the
 // data being benign. The log-sum-exp output is converted back to natural log.
 //
-// LDS layouts:
+// LDS layouts (a tile is contiguous 16-byte slots, padding included; a wave's
+// direct load fills 64 consecutive slots, and a lane whose slot is padding
+// fetches an in-range chunk of the same row that nobody reads):
 //   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272
 //       (or 144) bytes apart and so cover all 64 banks once.
 //   V [BN][D + 32]: row-major, rows 64 bytes apart modulo 256. V^T fragments
@@ -96,9 +101,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   constexpr int KST = D + 8;   // K row stride in LDS, elements
   constexpr int VST = D + 32;  // V row stride in LDS, elements
   constexpr int KCH = D / 8;   // 16-byte chunks per K/V row
-  constexpr int K_ROWS = NT / KCH;
-  constexpr int K_PASSES = BN / K_ROWS;  // K rows per thread, K_ROWS apart
-  constexpr int V_RPT = BN * KCH / NT;   // consecutive V rows per thread
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
@@ -167,35 +169,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  // ---- tile staging: K rows by 16-byte chunk, V rows V_RPT at a time
-  const int kc = tid % KCH, kr = tid / KCH;
-  const int vr = kr * V_RPT;
-  const int koff = (kr * (int)a.kss + kc * 8) * (int)sizeof(T);  // byte offset of this lane's first K chunk
-  const int voff = (vr * (int)a.vss + kc * 8) * (int)sizeof(T);
-  uint4 kreg[K_PASSES], vreg[V_RPT];
+  // ---- tile staging straight into LDS: a padded tile is KSLOTS (VSLOTS)
+  // 16-byte slots, slot s of a wave instruction landing at its base + 16*lane;
+  // the lane fetches the global chunk its slot holds (pad slots fetch an
+  // in-range chunk of the same row, which nobody reads)
+  constexpr int KSPR = KST / 8, VSPR = VST / 8;  // slots per padded row
+  constexpr int KSLOTS = BN * KSPR, VSLOTS = BN * VSPR;
+  constexpr int KI = (KSLOTS + NT - 1) / NT, VI = (VSLOTS + NT - 1) / NT;
+  int kgo[KI], vgo[VI];
+#pragma unroll
+  for (int i = 0; i < KI; ++i) {
+    const int sl = i * NT + tid, row = sl / KSPR, col = sl % KSPR;
+    kgo[i] = (row * (int)a.kss + (col < KCH ? col : col - (KSPR - KCH)) * 8) * (int)sizeof(T);
+  }
+#pragma unroll
+  for (int i = 0; i < VI; ++i) {
+    const int sl = i * NT + tid, row = sl / VSPR, col = sl % VSPR;
+    vgo[i] = (row * (int)a.vss + (col < KCH ? col : col - (VSPR - KCH)) * 8) * (int)sizeof(T);
+  }
   // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
   // dims 16kk + 8g ..), and the transposing V reads (see pv)
   const int k_lane = r32 * KST + 8 * g;
   const int v_lane = (4 * g + ((lane & 15) >> 2)) * VST + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  auto load_k = [&](int t) {
+  // tile t of K into Ks[buf] / of V into Vs[buf], asynchronously (vmcnt)
+  auto dma_k = [&](int t, int buf) {
     const int tile = t * BN * (int)a.kss * (int)sizeof(T);
 #pragma unroll
-    for (int p = 0; p < K_PASSES; ++p) kreg[p] = ld_buf(krsrc, koff + p * K_ROWS * (int)a.kss * (int)sizeof(T), tile);
+    for (int i = 0; i < KI; ++i)
+      if (KSLOTS % NT == 0 || i * NT + tid < KSLOTS)
+        ld_buf_lds(krsrc, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], tile);
   };
-  auto load_v = [&](int t) {
+  auto dma_v = [&](int t, int buf) {
     const int tile = t * BN * (int)a.vss * (int)sizeof(T);
 #pragma unroll
-    for (int i = 0; i < V_RPT; ++i) vreg[i] = ld_buf(vrsrc, voff + i * (int)a.vss * (int)sizeof(T), tile);
+    for (int i = 0; i < VI; ++i)
+      if (VSLOTS % NT == 0 || i * NT + tid < VSLOTS)
+        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
   };
-  auto store_k = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < K_PASSES; ++p) *reinterpret_cast<uint4*>(Ks[buf] + (kr + p * K_ROWS) * KST + kc * 8) = kreg[p];
-  };
-  auto store_v = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < V_RPT; ++i) *reinterpret_cast<uint4*>(Vs[buf] + (vr + i) * VST + kc * 8) = vreg[i];
-  };
+  auto landed = [&]() { lds_loads_landed(); };
   // S^T of the K tile in buffer buf
   auto scores = [&](int buf) {
     const T* ks = Ks[buf];
@@ -259,12 +271,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
   // ---- fast sweep: fixed max, S(t+1) pipelined with the softmax and PV of tile t
   clear();
-  load_k(0);
-  load_v(0);
-  store_k(0);
-  store_v(0);
-  load_k(1);  // past the end this reads zeros or keys nobody uses
-  store_k(1);
+  dma_k(0, 0);
+  dma_v(0, 0);
+  dma_k(1, 1);  // past the end this reads zeros or keys nobody uses
+  landed();
   __syncthreads();
   f32x16 sa = scores(0), sb;
   if (need_mask(0)) apply_mask(0, sa);
@@ -280,14 +290,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // V(t) in Vs[t&1] are read; K(t+2) goes to Ks[t&1] and V(t+1) to
   // Vs[(t+1)&1], whose previous tiles were last read in step t-1.
   auto step = [&](int t, f32x16& cur, f32x16& nxt) {
+    dma_k(min(t + 2, n_tiles), t & 1);
+    dma_v(min(t + 1, n_tiles - 1), (t + 1) & 1);
     if (need_mask(t)) apply_mask(t, cur);
-    load_k(t + 2);
-    load_v(min(t + 1, n_tiles - 1));
     nxt = scores((t + 1) & 1);
     softmax(cur, m_i, pf);
     pv(t & 1, pf);
-    store_k(t & 1);
-    store_v((t + 1) & 1);
+    landed();
     __syncthreads();
   };
   // pairs of steps keep each S in fixed registers; one exit keeps O in place
@@ -307,14 +316,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
       // same max in both)
       clear();
       m_i = -INFINITY;
-      load_k(0);
-      load_v(0);
-      store_k(0);
-      store_v(0);
+      dma_k(0, 0);
+      dma_v(0, 0);
+      landed();
       __syncthreads();
       for (int u = 0; u < n_tiles; ++u) {
-        load_k(min(u + 1, n_tiles - 1));
-        load_v(min(u + 1, n_tiles - 1));
+        dma_k(min(u + 1, n_tiles - 1), (u + 1) & 1);
+        dma_v(min(u + 1, n_tiles - 1), (u + 1) & 1);
         f32x16 s = scores(u & 1);
         if (need_mask(u)) apply_mask(u, s);
         float mx = -INFINITY;
@@ -333,8 +341,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         }
         softmax(s, m_i == -INFINITY ? 0.f : m_i, pf);
         pv(u & 1, pf);
-        store_k((u + 1) & 1);
-        store_v((u + 1) & 1);
+        landed();
         __syncthreads();
       }
     }
