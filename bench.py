@@ -52,7 +52,7 @@ MEASURED_TRAFFIC: dict[str, int | None] = {
     "add_rmsnorm": 4_314_051_694,
     "rope": 337_726_126,
     "qk_norm_rope": 510_771_483,
-    "attn_bwd": 15_115_471_835,  # the dq and dk/dv kernels of one pk_attn_bwd call
+    "attn_bwd": 5_920_925_584,  # the dq and dk/dv kernels of one pk_attn_bwd call
     "copy": 1_073_766_308,
 }
 
@@ -401,7 +401,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
         o, lse = impls.attn_with_lse(q, k, v, True)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        dsum = torch.empty_like(lse)
+        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=dev)
         strides = (_lib._i64 * 24)(*(s for t in (q, k, v, o, do, dq, dk, dv) for s in t.stride()[:3]))
 
         def step(i):

@@ -214,8 +214,8 @@ int pk_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, flo
 /*
  * Attention backward for pk_attn_fwd: given o, the upstream gradient dout
  * (like o) and the forward's lse, writes dq (like q), dk and dv (like k, v).
- * dsum is caller scratch shaped like lse (fp32 [batch, q_heads, seq]); it
- * receives D = rowsum(dout * o). Arithmetic: P is recomputed from q, k and
+ * dsum is caller scratch of twice lse's size (fp32 [2, batch, q_heads, seq]);
+ * it receives D = rowsum(dout * o), then lse * log2(e). Arithmetic: P is recomputed from q, k and
  * lse; dS = P (dP - D); dq = scale dS k, dk = scale dS^T q (summed over the q
  * heads of each kv head), dv = P^T dout; fp32 accumulation, one rounding per
  * output, no atomics (the result is deterministic). strides[24] = q, k, v, o,
@@ -228,8 +228,8 @@ int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 void* stream);
 
 /*
- * Backward of pk_attn_varlen_fwd (packed sequences). lse and dsum are fp32
- * [q_heads, total]; strides[16] = q, k, v, o, dout, dq, dk, dv (token, head).
+ * Backward of pk_attn_varlen_fwd (packed sequences). lse is fp32
+ * [q_heads, total] and dsum fp32 [2, q_heads, total]; strides[16] = q, k, v, o, dout, dq, dk, dv (token, head).
  * Replaces torch autograd of the reference `attn_varlen`
  * (kernels/attn_varlen.py:41-54).
  */

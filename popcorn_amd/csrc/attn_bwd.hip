@@ -7,25 +7,39 @@
 //               recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //               P = exp2(s*c - lse2) from the forward's log-sum-exp and
 //               dS = P (dP - D), and accumulates dQ^T += K^T dS^T. Its prologue
-//               also computes D = rowsum(dO * O) for its rows and stores it for
-//               the second kernel.
-//   dkdv kernel one block = 4 waves x 32 keys of one (sequence, kv head),
-//               holding its K and V fragments in registers; query tiles of 32
-//               rows (over every q head of the group) stream through LDS. Per
-//               tile each wave computes S = Q K^T and dP = dO V^T, whose result
-//               layout puts one key per lane column, so P and dS go straight
-//               into dV^T += dO^T P and dK^T += Q^T dS as B operands.
+//               also computes D = rowsum(dO * O) for its rows and stores it,
+//               with lse2 = lse * log2(e), for the second kernel.
+//   dkdv kernel one block = 128 keys of one (sequence, kv head) in four
+//               32-key slices, two waves per slice sharing a SIMD; query tiles
+//               of 32 rows (over every q head of the group) stream through
+//               LDS. The slice's role-0 wave holds K and computes S = Q K^T,
+//               whose result layout puts one key per lane column, so
+//               P = exp2(s*c - lse2) goes straight into dV^T += dO^T P as the
+//               B operand; it also leaves P (fp32) in LDS. The role-1 wave
+//               holds V, computes dP = dO V^T one step later, reads that P,
+//               forms dS = P (dP - D) and accumulates dK^T += Q^T dS. Splitting
+//               the roles halves each wave's registers (one fragment set, one
+//               accumulator), which is what lets two waves share each SIMD.
+//               Query tiles (with their lse2 and D rows) arrive two steps ahead
+//               through four LDS stages.
+//
+// Both kernels stage tiles with buffer loads that write LDS directly (16
+// bytes per lane at the wave's LDS base + 16 * lane): each lane fetches the
+// global chunk that its LDS slot holds under the swizzle below, so no staging
+// registers or LDS stores are needed. Rows past the end read as zero.
 //
 // With scores z = scale * q.k: dS = dL/dz, dQ = scale * dS K,
-// dK = scale * dS^T Q, dV = P^T dO. A negative scale is applied as in the
-// forward (Q negated on load, c = |scale| log2 e), so dK uses |scale| and
-// dQ the signed scale.
+// dK = scale * dS^T Q, dV = P^T dO. In the dq kernel a negative scale is
+// applied as in the forward (Q negated on load, c = |scale| log2 e), so dQ
+// takes the signed scale; the dkdv kernel stages Q unchanged and uses the
+// signed c and the signed scale for dK.
 //
-// LDS tiles are row-major 16-byte chunks. For head_dim 128 chunk c of row r
-// sits at c ^ (4 (r % 4) + (r / 4) % 4): the 16-byte fragment reads (16 rows,
-// one chunk) and the transposing ds_read_b64_tr_b16 reads (4 rows x 4 chunks
-// per pair of 16-lane groups) both land on 64 distinct banks. head_dim 64
-// rows are padded to 72 elements instead.
+// LDS tiles are unpadded rows of 16-byte chunks, chunk c of row r stored at
+// c ^ swz(r): swz(r) = 4 (r % 4) + (r / 4) % 4 for head_dim 128 (rows span all
+// 64 banks) and 4 ((r / 2) % 2) + (r / 4) % 4 for head_dim 64 (two rows per
+// bank sweep). Either way the 16-byte fragment reads (16 rows, one chunk) and
+// the transposing ds_read_b64_tr_b16 reads (4 rows x 4 chunks per pair of
+// 16-lane groups) land on 64 distinct banks.
 #include <math.h>
 
 #include "api.h"
@@ -51,20 +65,25 @@ struct BwdArgs {
   int total;
   int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];  // (batch, token, head) strides
   int64_t lse_bs, lse_hs;
+  int64_t lse_n;  // elements of lse; dsum[lse_n + i] holds lse[i] * log2(e)
   int B, S, Hq, Hkv, group;
   float scale;  // signed softmax scale
   float c;      // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;
 };
 
-// LDS tile layout: element offset of (row, dim), dim a multiple of 4
+// LDS tile layout: unpadded rows, 16-byte chunk c of row r at c ^ swz(r)
 template <int D> struct Tile {
-  static constexpr int ST = D == 128 ? 128 : D + 8;
-  static __device__ __forceinline__ int at(int row, int dim) {
+  static constexpr int ST = D;
+  static __device__ __forceinline__ int swz(int row) {
     if constexpr (D == 128)
-      return row * 128 + ((((dim >> 3) ^ (4 * (row & 3) + ((row >> 2) & 3))) << 3) | (dim & 7));
+      return 4 * (row & 3) + ((row >> 2) & 3);
     else
-      return row * ST + dim;
+      return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+  }
+  // element offset of (row, dim), dim a multiple of 4
+  static __device__ __forceinline__ int at(int row, int dim) {
+    return row * D + ((((dim >> 3) ^ swz(row)) << 3) | (dim & 7));
   }
 };
 
@@ -87,20 +106,32 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
   constexpr int KCH = D / 8;
-  constexpr int ROWS = NT / KCH;     // tile rows staged per pass
-  constexpr int PASSES = BN / ROWS;  // 2 (D = 128) or 1 (D = 64)
+  constexpr int TI = BN * KCH / NT;  // direct loads per thread per tile of K (and of V): 2 or 1
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * L::ST];
   __shared__ __attribute__((aligned(16))) T Vs[2][BN * L::ST];
 
+  // work item: (q tile, batch, kv head) groups, longest causal rows first; the
+  // q heads of a group are adjacent on one XCD (dispatch is round-robin over
+  // the 8 XCDs), so their shared K/V tiles are fetched into that XCD's L2 once
   const int m_tiles = (a.S + BM - 1) / BM;
+  const int G = a.group;
   const int w = blockIdx.x;
-  const int per_tile = a.B * a.Hq;
-  const int m_tile = m_tiles - 1 - w / per_tile;  // longest causal rows first
-  const int b = (w % per_tile) / a.Hq;
-  const int hq = w % a.Hq;
-  const int hkv = hq / a.group;
+  int gidx, hig;
+  if (gridDim.x % (8 * G) == 0) {
+    const int wp = w >> 3;
+    gidx = (wp / G) * 8 + (w & 7);
+    hig = wp % G;
+  } else {
+    gidx = w / G;
+    hig = w % G;
+  }
+  const int per_tile = a.B * a.Hkv;
+  const int m_tile = m_tiles - 1 - gidx / per_tile;
+  const int b = (gidx % per_tile) / a.Hkv;
+  const int hkv = gidx % a.Hkv;
+  const int hq = hkv * G + hig;
   int start, S;
   seq_bounds(a, b, start, S);
   const int m0 = m_tile * BM;
@@ -147,27 +178,28 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int64_t lidx = b * a.lse_bs + hq * a.lse_hs + start + q_row;
   // rows past the end: lse2 = +inf makes every p zero
   const float lse2 = row_ok ? a.lse[lidx] * 1.4426950408889634f : INFINITY;
-  if (row_ok && g == 0) a.dsum[lidx] = dsum;
+  if (row_ok && g == 0) {
+    a.dsum[lidx] = dsum;
+    a.dsum[a.lse_n + lidx] = lse2;
+  }
 
   const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  const int kc = tid % KCH, kr = tid / KCH;
-  uint4 kreg[PASSES], vreg[PASSES];
-  auto load = [&](int t) {
+  // staging straight into LDS: slot i*NT + tid of a tile is row sl / KCH,
+  // stored chunk sl % KCH, which holds logical chunk (sl % KCH) ^ swz(row)
+  int kgo[TI], vgo[TI];
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int row = t * BN + kr + p * ROWS;
-      kreg[p] = ld_buf(krsrc, (kc * 8) * (int)sizeof(T), row * (int)a.ks[1] * (int)sizeof(T));
-      vreg[p] = ld_buf(vrsrc, (kc * 8) * (int)sizeof(T), row * (int)a.vs[1] * (int)sizeof(T));
-    }
-  };
-  auto store = [&](int buf) {
+  for (int i = 0; i < TI; ++i) {
+    const int sl = i * NT + tid, row = sl / KCH, c = (sl % KCH) ^ L::swz(row);
+    kgo[i] = (row * (int)a.ks[1] + c * 8) * (int)sizeof(T);
+    vgo[i] = (row * (int)a.vs[1] + c * 8) * (int)sizeof(T);
+  }
+  auto issue = [&](int t, int buf) {
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int off = L::at(kr + p * ROWS, kc * 8);
-      *reinterpret_cast<uint4*>(Ks[buf] + off) = kreg[p];
-      *reinterpret_cast<uint4*>(Vs[buf] + off) = vreg[p];
+    for (int i = 0; i < TI; ++i) {
+      ld_buf_lds(krsrc, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(T));
+      ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(T));
     }
   };
   // lane offsets: K / V fragment kk (A operand: row r32, dims 16kk + 8g) and the
@@ -187,12 +219,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  load(0);
-  store(0);
+  issue(0, 0);
+  lds_loads_landed();
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
-    load(min(t + 1, n_tiles - 1));
+    issue(min(t + 1, n_tiles - 1), buf ^ 1);  // its previous tile was last read in step t - 1
     const int kv0 = t * BN;
     if (!(CAUSAL && kv0 > wave_first + 31)) {
       const T* ks = Ks[buf];
@@ -228,7 +260,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
                                 dsf[c], acc[dt]);
         }
     }
-    store(buf ^ 1);
+    lds_loads_landed();
     __syncthreads();
   }
 
@@ -246,25 +278,31 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 // ---------------------------------------------------------------- dkdv kernel
 
+constexpr int NT2 = 512;  // dkdv kernel: 8 waves, two per SIMD
+
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1))) void attn_bwd_dkdv_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(2))) void attn_bwd_dkdv_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
-  constexpr int KCH = D / 8;
-  constexpr int PER = BQ * KCH / NT;  // chunks of each of Q and dO per thread: 2 (D = 128) or 1
+  constexpr int KCH = D / 8;             // 16-byte chunks per row
+  constexpr int SLOTS = BQ * KCH;        // 16-byte slots of a Q (or dO) tile: 512 or 256
+  constexpr int TI = 2 * SLOTS / NT2;    // direct loads per thread per tile (Q and dO together): 2 or 1
+  constexpr int NS = 4;                  // query tiles resident or in flight in LDS
+  constexpr int PER_ISSUE = TI + 1;      // loads each wave issues per tile (tiles, one row vector)
+  constexpr int TILE = BQ * D;
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Qs[2][BQ * L::ST];
-  __shared__ __attribute__((aligned(16))) T Gs[2][BQ * L::ST];
-  __shared__ __attribute__((aligned(16))) float Ls[2][BQ];  // lse2 of the tile's rows (+inf past the end)
-  __shared__ __attribute__((aligned(16))) float Dsm[2][BQ];
+  // stage: Q tile then dO tile; row vectors: lse2, then D (64 slots: whole-wave loads)
+  __shared__ __attribute__((aligned(16))) T QG[NS][2 * TILE];
+  __shared__ __attribute__((aligned(16))) float RV[NS][2][64];
+  __shared__ __attribute__((aligned(16))) float spill[64];
+  // P of each key slice, fp32, double-buffered: [buffer][slice][16 values x 64 lanes]
+  __shared__ __attribute__((aligned(16))) float Pb[2][4][16 * 64];
 
-  const int kv_tiles = (a.S + BK - 1) / BK;
   const int w = blockIdx.x;
   const int per_tile = a.B * a.Hkv;
   const int kv_tile = w / per_tile;  // first key tiles (the most causal work) first
-  (void)kv_tiles;
   const int b = (w % per_tile) / a.Hkv;
   const int hkv = w % a.Hkv;
   int start, S;
@@ -274,74 +312,73 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // waves w and w + 4 share a SIMD and a key slice: role 0 (waves 0-3) forms
+  // P from S = Q K^T and accumulates dV; role 1 (waves 4-7) forms dS from
+  // dP = dO V^T and the P role 0 left in LDS, and accumulates dK
+  const int role = wave >> 2;
+  const int slice = wave & 3;
   const int lane = tid & 63;
   const int r32 = lane & 31;
   const int g = lane >> 5;
-  const int kw0 = kb0 + wave * 32;
+  const int kw0 = kb0 + slice * 32;
   const int key = kw0 + r32;
   const bool key_ok = key < S;
 
-  // this lane's key as the B operand of S = Q K^T and dP = dO V^T
-  Frag kf[KK], vf[KK];
+  // this lane's key row as the B operand: K (role 0) or V (role 1)
+  Frag bf[KK];
   {
-    const T* krow = static_cast<const T*>(a.k) + b * a.ks[0] + hkv * a.ks[2] + (int64_t)(start + key) * a.ks[1];
-    const T* vrow = static_cast<const T*>(a.v) + b * a.vs[0] + hkv * a.vs[2] + (int64_t)(start + key) * a.vs[1];
+    const T* row = role == 0
+                       ? static_cast<const T*>(a.k) + b * a.ks[0] + hkv * a.ks[2] + (int64_t)(start + key) * a.ks[1]
+                       : static_cast<const T*>(a.v) + b * a.vs[0] + hkv * a.vs[2] + (int64_t)(start + key) * a.vs[1];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      uint4 kr = make_uint4(0, 0, 0, 0), vr = kr;
-      if (key_ok) {
-        kr = *reinterpret_cast<const uint4*>(krow + 16 * kk + 8 * g);
-        vr = *reinterpret_cast<const uint4*>(vrow + 16 * kk + 8 * g);
-      }
-      kf[kk] = __builtin_bit_cast(Frag, kr);
-      vf[kk] = __builtin_bit_cast(Frag, vr);
+      uint4 r = make_uint4(0, 0, 0, 0);
+      if (key_ok) r = *reinterpret_cast<const uint4*>(row + 16 * kk + 8 * g);
+      bf[kk] = __builtin_bit_cast(Frag, r);
     }
   }
+  // Q is staged unflipped: a negative scale signs the exponent's coefficient
+  // here and dK's final scale
+  const float cs = a.q_flip ? -a.c : a.c;
 
   // query tiles: every q head of the group, rows from the block's first key on (causal)
   const int u0 = CAUSAL ? kb0 / BQ : 0;
   const int n_u = (S + BQ - 1) / BQ - u0;
   const int n_it = a.group * n_u;
 
-  const int kc = tid % KCH, kr = tid / KCH;  // staging: row kr (+ NT / KCH per pass), chunk kc
-  constexpr int ROWS = NT / KCH;
-  uint4 qreg[PER], greg[PER];
-  float lreg = INFINITY, dreg = 0.f;
-  auto load = [&](int it) {
-    const int hq = hkv * a.group + it / n_u;
-    const int u = u0 + it % n_u;
+  // staging: slot sl = i*NT2 + tid of the stage (Q slots, then dO slots) is
+  // row (sl % SLOTS) / KCH of that tile, stored chunk sl % KCH, which holds
+  // logical chunk (sl % KCH) ^ swz(row); a wave's 64 slots lie in one tile
+  int go[TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const int sl = i * NT2 + tid, op = sl / SLOTS, within = sl % SLOTS;
+    const int row = within / KCH, c = (within % KCH) ^ L::swz(row);
+    go[i] = (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T);
+  }
+  // tile `it` (clamped: past the end it reloads the last tile) into stage st
+  auto issue = [&](int it, int st) {
+    const int itc = min(it, n_it - 1);
+    const int hq = hkv * a.group + itc / n_u;
+    const int r0 = (u0 + itc % n_u) * BQ;
     const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const T* gb = static_cast<const T*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
-    const __amdgpu_buffer_rsrc_t qrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)qb, (short)0, (int)(((int64_t)(S - 1) * a.qs[1] + D) * (int)sizeof(T)),
-                                          0x00020000);
-    const __amdgpu_buffer_rsrc_t grs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)gb, (short)0, (int)(((int64_t)(S - 1) * a.gs[1] + D) * (int)sizeof(T)),
-                                          0x00020000);
+    const float* db = a.dsum + b * a.lse_bs + hq * a.lse_hs + start;
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int row = u * BQ + kr + p * ROWS;
-      qreg[p] = flip(ld_buf(qrs, kc * 8 * (int)sizeof(T), row * (int)a.qs[1] * (int)sizeof(T)), a.q_flip);
-      greg[p] = ld_buf(grs, kc * 8 * (int)sizeof(T), row * (int)a.gs[1] * (int)sizeof(T));
+    for (int i = 0; i < TI; ++i) {
+      const int first = i * NT2 + wave * 64;  // wave-uniform
+      const bool isq = first < SLOTS;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(isq ? qb : gb), (short)0,
+          (int)(((int64_t)(S - 1) * (isq ? a.qs[1] : a.gs[1]) + D) * (int)sizeof(T)), 0x00020000);
+      ld_buf_lds(rs, QG[st] + first * 8, go[i], r0 * (int)(isq ? a.qs[1] : a.gs[1]) * (int)sizeof(T));
     }
-    if (tid < BQ) {
-      const int row = u * BQ + tid;
-      const int64_t li = b * a.lse_bs + hq * a.lse_hs + start + row;
-      lreg = row < S ? a.lse[li] * 1.4426950408889634f : INFINITY;
-      dreg = row < S ? a.dsum[li] : 0.f;
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int off = L::at(kr + p * ROWS, kc * 8);
-      *reinterpret_cast<uint4*>(Qs[buf] + off) = qreg[p];
-      *reinterpret_cast<uint4*>(Gs[buf] + off) = greg[p];
-    }
-    if (tid < BQ) {
-      Ls[buf][tid] = lreg;
-      Dsm[buf][tid] = dreg;
-    }
+    // rows past the end read as zero; their p is masked. wave 0: lse2 of the
+    // rows; wave 1: D; the other waves repeat D into `spill`
+    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(wave == 0 ? db + a.lse_n : db), (short)0, S * (int)sizeof(float), 0x00020000);
+    ld_buf_lds4(rrs, wave == 0 ? RV[st][0] : (wave == 1 ? RV[st][1] : spill), lane * (int)sizeof(float),
+                r0 * (int)sizeof(float));
   };
 
   int a_lane[KK], t_lane[2][DT];
@@ -353,94 +390,127 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     for (int dt = 0; dt < DT; ++dt)
       t_lane[hi][dt] = L::at(8 * hi + 4 * g + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
 
-  f32x16 dv[DT], dk[DT];
+  f32x16 acc[DT];  // dV (role 0) or dK (role 1)
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dv[dt][r] = dk[dt][r] = 0.f;
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  load(0);
-  store(0);
+  // 16 x 32 score block of the tile in stage st against this slice's keys,
+  // A operand from `base` (Q for role 0, dO for role 1)
+  auto product = [&](const T* base) {
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) s = Mma<T>::run(*reinterpret_cast<const Frag*>(base + a_lane[kk]), bf[kk], s);
+    return s;
+  };
+  // acc^T += X^T F with X^T fragments from transposing reads of the tile at `base`
+  auto accumulate = [&](const T* base, const Frag (&f)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + t_lane[0][dt] + 16 * c * L::ST));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + t_lane[1][dt] + 16 * c * L::ST));
+        acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), f[c],
+                              acc[dt]);
+      }
+  };
+  // this lane's 16 values of a tile's row vector v (rows 8j + 4g + i, r = 4j + i)
+  auto rows16 = [&](const float* v, float (&out)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 x = *reinterpret_cast<const float4*>(v + 8 * j + 4 * g);
+      out[4 * j] = x.x;
+      out[4 * j + 1] = x.y;
+      out[4 * j + 2] = x.z;
+      out[4 * j + 3] = x.w;
+    }
+  };
+  // P buffer layout: value r of lane l at (r / 4) * 256 + 4 * l + r % 4 (16-byte lane stride)
+  float* pmine = nullptr;
+
+  // Step t: role 0 takes tile t (P into Pb[t & 1]), role 1 tile t - 1 (P from
+  // Pb[(t - 1) & 1]). Tile t + NS - 2 is issued into the stage of tile t - 2,
+  // which role 1 finished in step t - 1; the step ends once tile t + 1 has landed.
+#pragma unroll
+  for (int j = 0; j < NS - 2; ++j) issue(j, j);
+  loads_landed_but<(NS - 3) * PER_ISSUE>();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    const int buf = it & 1;
-    load(min(it + 1, n_it - 1));
-    const int q0 = (u0 + it % n_u) * BQ;
-    // skip tiles whose every query precedes every key of this wave
-    if (!(CAUSAL && q0 + BQ - 1 < kw0)) {
-      const T* qs = Qs[buf];
-      const T* gs = Gs[buf];
-      f32x16 s, dp;
+  (void)pmine;
+  for (int t = 0; t <= n_it; ++t) {
+    issue(t + NS - 2, (t + NS - 2) % NS);
+    if (role == 0) {
+      if (t < n_it) {
+        const int st = t % NS;
+        const T* qs = QG[st];
+        const f32x16 s = product(qs);
+        const int q0 = (u0 + t % n_u) * BQ;
+        float l2[16];
+        rows16(RV[st][0], l2);
+        // tiles wholly before this slice's keys (causal) are masked to zero, not skipped
+        const bool need_mask = (CAUSAL && q0 < kw0 + 32) || !key_ok || q0 + BQ > S;
+        float p[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        s = Mma<T>::run(*reinterpret_cast<const Frag*>(qs + a_lane[kk]), kf[kk], s);
-        dp = Mma<T>::run(*reinterpret_cast<const Frag*>(gs + a_lane[kk]), vf[kk], dp);
-      }
-      // this lane's 16 queries: rows 8j + 4g + i of the tile (r = 4j + i)
-      float l2[16], dd[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 lv = *reinterpret_cast<const float4*>(&Ls[buf][8 * j + 4 * g]);
-        const float4 dv4 = *reinterpret_cast<const float4*>(&Dsm[buf][8 * j + 4 * g]);
-        l2[4 * j] = lv.x;
-        l2[4 * j + 1] = lv.y;
-        l2[4 * j + 2] = lv.z;
-        l2[4 * j + 3] = lv.w;
-        dd[4 * j] = dv4.x;
-        dd[4 * j + 1] = dv4.y;
-        dd[4 * j + 2] = dv4.z;
-        dd[4 * j + 3] = dv4.w;
-      }
-      const bool need_mask = (CAUSAL && q0 < kw0 + 32) || !key_ok;
-      Frag pf[2], dsf[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = 8 * c + j;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.c, -l2[r]));
+        for (int r = 0; r < 16; ++r) {
+          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], cs, -l2[r]));
           if (need_mask) {
             const int qrow = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            p = key_ok && (!CAUSAL || key <= qrow) ? p : 0.f;
+            p[r] = key_ok && qrow < S && (!CAUSAL || key <= qrow) ? p[r] : 0.f;
           }
-          pf[c][j] = (T)p;
-          dsf[c][j] = (T)(p * (dp[r] - dd[r]));
         }
-      // dV^T += dO^T P and dK^T += Q^T dS, A operands from transposing reads
+        float* pw = Pb[t & 1][slice];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<float4*>(pw + 256 * j + 4 * lane) = make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
+        Frag pf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pf[c][j] = (T)p[8 * c + j];
+        accumulate(qs + TILE, pf);  // dV^T += dO^T P
+      }
+    } else if (t > 0) {
+      const int u = t - 1;
+      const int st = u % NS;
+      const T* qs = QG[st];
+      const f32x16 dp = product(qs + TILE);
+      float dd[16], p[16];
+      rows16(RV[st][1], dd);
+      const float* pr = Pb[u & 1][slice];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 x = *reinterpret_cast<const float4*>(pr + 256 * j + 4 * lane);
+        p[4 * j] = x.x;
+        p[4 * j + 1] = x.y;
+        p[4 * j + 2] = x.z;
+        p[4 * j + 3] = x.w;
+      }
+      Frag dsf[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const s16x4 glo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(gs + t_lane[0][dt] + 16 * c * L::ST));
-          const s16x4 ghi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(gs + t_lane[1][dt] + 16 * c * L::ST));
-          dv[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(glo, ghi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                               pf[c], dv[dt]);
-          const s16x4 qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(qs + t_lane[0][dt] + 16 * c * L::ST));
-          const s16x4 qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(qs + t_lane[1][dt] + 16 * c * L::ST));
-          dk[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                               dsf[c], dk[dt]);
-        }
+        for (int j = 0; j < 8; ++j) dsf[c][j] = (T)(p[8 * c + j] * (dp[8 * c + j] - dd[8 * c + j]));
+      accumulate(qs, dsf);  // dK^T += Q^T dS
     }
-    store(buf ^ 1);
+    loads_landed_but<(NS - 3) * PER_ISSUE>();
     __syncthreads();
   }
+  loads_landed_but<0>();  // tiles issued past the end, before the block's LDS is released
 
   if (key_ok) {
-    const float ks = fabsf(a.scale);
-    T* dkrow = static_cast<T*>(a.dk) + b * a.dks[0] + hkv * a.dks[2] + (int64_t)(start + key) * a.dks[1];
-    T* dvrow = static_cast<T*>(a.dv) + b * a.dvs[0] + hkv * a.dvs[2] + (int64_t)(start + key) * a.dvs[1];
+    T* out = role == 0
+                 ? static_cast<T*>(a.dv) + b * a.dvs[0] + hkv * a.dvs[2] + (int64_t)(start + key) * a.dvs[1]
+                 : static_cast<T*>(a.dk) + b * a.dks[0] + hkv * a.dks[2] + (int64_t)(start + key) * a.dks[1];
+    const float f = role == 0 ? 1.0f : a.scale;  // dK: signed scale, Q was staged unflipped
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = dt * 32 + 8 * rq + 4 * g;
-        *reinterpret_cast<uint2*>(dvrow + d0) =
-            pack4<T>(dv[dt][4 * rq], dv[dt][4 * rq + 1], dv[dt][4 * rq + 2], dv[dt][4 * rq + 3]);
-        *reinterpret_cast<uint2*>(dkrow + d0) = pack4<T>(dk[dt][4 * rq] * ks, dk[dt][4 * rq + 1] * ks,
-                                                         dk[dt][4 * rq + 2] * ks, dk[dt][4 * rq + 3] * ks);
-      }
+      for (int rq = 0; rq < 4; ++rq)
+        *reinterpret_cast<uint2*>(out + dt * 32 + 8 * rq + 4 * g) =
+            pack4<T>(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
   }
 }
 
@@ -450,10 +520,10 @@ int launch(const BwdArgs& a, bool causal, hipStream_t s) {
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv;
   if (causal) {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, true>), dim3(kv_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, true>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   } else {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false>), dim3(kv_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   }
   return launched("pk_attn_bwd");
 }
@@ -527,6 +597,7 @@ int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   a.cu = nullptr;
   a.lse_bs = q_heads * seq;  // [batch, q_heads, seq]
   a.lse_hs = seq;
+  a.lse_n = batch * q_heads * seq;
   return bwd_launch("pk_attn_bwd", a, strides, batch, seq, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
                     stream);
 }
@@ -564,6 +635,7 @@ int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* 
   a.total = (int)total;
   a.lse_bs = 0;  // [q_heads, total]
   a.lse_hs = total;
+  a.lse_n = q_heads * total;
   return bwd_launch(who, a, dense, num_seqs, max_seqlen, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
                     stream);
 }

@@ -44,8 +44,19 @@ __device__ __forceinline__ void ld_buf_lds(__amdgpu_buffer_rsrc_t r, void* lds, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
 }
 
+// 4 bytes per lane, as ld_buf_lds (lane i's word at lds + 4 * i).
+__device__ __forceinline__ void ld_buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds, int voffset, int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voffset, soffset, 0, 0);
+}
+
 // Wait until this wave's LDS-bound buffer loads have landed.
 __device__ __forceinline__ void lds_loads_landed() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Wait until at most N of this wave's vector memory loads are still in flight
+// (they complete in issue order).
+template <int N> __device__ __forceinline__ void loads_landed_but() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // Four 16-bit values as two packed 32-bit words
 template <typename T> __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {

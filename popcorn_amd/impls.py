@@ -549,7 +549,7 @@ class _Attention(torch.autograd.Function):
         q_, k_, v_, do_ = (_aligned_rows(t) for t in (q, k, v, do.to(q.dtype)))
         dq, dk, dv = torch.empty(q.shape, dtype=q.dtype, device=q.device), torch.empty_like(k_), torch.empty_like(v_)
         dk, dv = dk.contiguous(), dv.contiguous()
-        dsum = torch.empty_like(lse)
+        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=lse.device)  # D, lse2
         lib = _lib.load()
         strides = (_lib._i64 * 24)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:3]))
         _lib.check(
@@ -649,7 +649,7 @@ class _AttentionVarlen(torch.autograd.Function):
         dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
         dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-        dsum = torch.empty_like(lse)
+        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=lse.device)  # D, lse2
         lib = _lib.load()
         strides = (_lib._i64 * 16)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:2]))
         _lib.check(
