@@ -146,3 +146,23 @@ def test_attn_fp16_long_uniform_rows():
     mean = v.double().mean(dim=1, keepdim=True).expand(b, s, hkv, d).repeat_interleave(hq // hkv, dim=2)
     assert (o.double() - mean).abs().max().item() < 2e-3
     assert (lse.double() - np.log(s)).abs().max().item() < 1e-4
+
+
+def test_attn_contiguous_views_at_odd_offsets():
+    """A contiguous tensor starting 2 bytes into its buffer is not 16-byte aligned: the wrapper copies it."""
+    b, s, hq, hkv, d = 1, 70, 4, 2, 128
+    flat = seeded((b * s * (hq + 2 * hkv) * d + 3,), 31, torch.bfloat16).to(DEV)
+    n_q, n_kv = b * s * hq * d, b * s * hkv * d
+    q = flat[1:1 + n_q].view(b, s, hq, d)
+    k = flat[1 + n_q:1 + n_q + n_kv].view(b, s, hkv, d)
+    v = flat[1 + n_q + n_kv:1 + n_q + 2 * n_kv].view(b, s, hkv, d)
+    assert q.is_contiguous() and q.data_ptr() % 16 != 0
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]  # aligned copies
+    want = impls.attn(*leaves, True)
+    want_grads = torch.autograd.grad(want, leaves, torch.ones_like(want))
+    odd = [t.detach().requires_grad_() for t in (q, k, v)]
+    got = impls.attn(*odd, True)
+    got_grads = torch.autograd.grad(got, odd, torch.ones_like(got))
+    assert torch.equal(got, want)
+    for a, c in zip(got_grads, want_grads):
+        assert torch.equal(a, c)

@@ -146,3 +146,21 @@ def test_qk_norm_rope_notebook_shape_against_fp32_torch():
             scale = max(1.0, ref.abs().max().item())
             tol = 2e-2 if name != "dw" else 1e-2  # dw sums 524288 rows in fp32 and rounds once
             assert err <= tol * scale, f"{name}: {err:.3e} vs scale {scale:.2f}"
+
+
+def test_qk_norm_rope_contiguous_views_at_odd_offsets():
+    """q, k and the weights starting 2 bytes into their buffers give the aligned result bit for bit."""
+    b, hq, hkv, s, d = 1, 4, 2, 40, 128
+    flat = seeded((b * (hq + hkv) * s * d + 2 * d + 5,), 41, torch.bfloat16).to(DEV)
+    n_q, n_k = b * hq * s * d, b * hkv * s * d
+    q = flat[1:1 + n_q].view(b, hq, s, d)
+    k = flat[1 + n_q:1 + n_q + n_k].view(b, hkv, s, d)
+    qw = flat[1 + n_q + n_k:1 + n_q + n_k + d]
+    kw = flat[1 + n_q + n_k + d:1 + n_q + n_k + 2 * d]
+    assert q.data_ptr() % 16 != 0 and qw.data_ptr() % 16 != 0
+    cos, sin = (t.to(torch.bfloat16).to(DEV) for t in tables(1, s, d, 42))
+    with torch.no_grad():
+        got = impls.qk_norm_rope(q, k, qw, kw, cos, sin)
+        want = impls.qk_norm_rope(q.clone(), k.clone(), qw.clone(), kw.clone(), cos, sin)
+    for a, c in zip(got, want):
+        assert torch.equal(a, c)
