@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libpopcorn_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
