@@ -98,3 +98,27 @@ def test_attn_varlen_long_packed_batch():
             got = o[lo:hi, h].cpu().double().numpy()[rows]
             assert np.abs(got - o64).max() < 2e-2 * max(1.0, np.abs(o64).max())
             np.testing.assert_allclose(lse[h, lo:hi].cpu().double().numpy()[rows], lse64, rtol=0, atol=1e-3)
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_attn_varlen_empty_segments(causal):
+    """Zero-length sequences (repeated offsets) produce nothing and leave the others exact, forward and backward."""
+    cu = torch.tensor([0, 0, 5, 5, 5, 40, 41, 41], dtype=torch.int32)
+    total, hq, hkv, d = 41, 4, 2, 64
+    q = seeded((total, hq, d), 61, torch.bfloat16).to(DEV)
+    k = seeded((total, hkv, d), 62, torch.bfloat16).to(DEV)
+    v = seeded((total, hkv, d), 63, torch.bfloat16).to(DEV)
+    do = seeded((total, hq, d), 64, torch.bfloat16).to(DEV)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    o = impls.attn_varlen(*leaves, cu.to(DEV), causal)
+    grads = torch.autograd.grad(o, leaves, do)
+    bounds = cu.tolist()
+    for lo, hi in zip(bounds, bounds[1:]):
+        if hi == lo:
+            continue
+        seg = [t[lo:hi][None].clone().requires_grad_() for t in (q, k, v)]
+        ref = impls.attn(*seg, causal)
+        ref_grads = torch.autograd.grad(ref, seg, do[lo:hi][None])
+        assert torch.equal(o[lo:hi], ref[0]), (lo, hi)
+        for g, r in zip(grads, ref_grads):
+            assert torch.equal(g[lo:hi], r[0]), (lo, hi)
