@@ -2,7 +2,7 @@
 // gfx950 matrix cores.
 //
 // Block = 4 wavefronts x 32 query rows (BM = 128) of one (batch, q head);
-// two blocks share a CU (two waves per SIMD). Keys stream through LDS in
+// three blocks share a CU (three waves per SIMD). Keys stream through LDS in
 // tiles of BN = 32.
 //
 // Per tile each wave computes
@@ -17,15 +17,16 @@
 // step is permuted identically in P^T and in the V^T fragments, which the
 // contraction does not see.
 //
-// Software pipeline (per wave): step t masks S(t), exponentiates it and
-// multiplies P(t) into O while the matrix cores compute S(t+1) from the
-// next K tile, so the softmax arithmetic of one tile overlaps the matrix
-// work of the next. Staging runs ahead of that: the step starts by issuing
-// K(t+2) and V(t+1) as buffer loads that write LDS directly (no staging
-// registers, no LDS stores), into buffers every wave has finished with, and
-// ends once they have landed; one barrier per step. Without staging
-// registers the head_dim-128 kernel fits three waves per SIMD (three blocks
-// per CU).
+// Per step (per wave): step t masks S(t) and exponentiates it into P(t),
+// then issues one run of matrix products, O += V(t)^T P(t)^T followed by
+// S(t+1) = K(t+1) Q^T written over S(t), whose LDS fragment reads run kRing
+// products ahead of their use. One S array (not two) leaves the registers
+// for that read-ahead, and the three waves that share a SIMD overlap one
+// wave's softmax with another's products. Staging runs ahead of that: the
+// step starts by issuing K(t+2) and V(t+1) as buffer loads that write LDS
+// directly (no staging registers, no LDS stores), into buffers every wave
+// has finished with, and ends once they have landed; one barrier per step.
+// The head_dim-128 kernel fits three waves per SIMD (three blocks per CU).
 //
 // Softmax with a fixed reference max: m is the row max of s * c over the
 // first key tile (key 0 is visible to every row) and stays put, so no step
@@ -41,7 +42,7 @@
 //
 // LDS layouts (a tile is contiguous 16-byte slots, padding included; a wave's
 // direct load fills 64 consecutive slots, and a lane whose slot is padding
-// fetches an in-range chunk of the same row that nobody reads):
+// reads past the buffer's range, which returns zeros without a memory access):
 //   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272
 //       (or 144) bytes apart and so cover all 64 banks once.
 //   V [BN][D + 32]: row-major, rows 64 bytes apart modulo 256. V^T fragments
@@ -72,6 +73,10 @@ using namespace attn;
 constexpr int BM = 128;
 constexpr int BN = 32;
 constexpr int NT = 256;
+constexpr int kRing = 6;  // fragment reads in flight ahead of the product that uses them
+// Buffer offset of a padding slot: at or past every range the kernel builds
+// (each below 2^31), and with a tile offset below 2^31 added it cannot wrap.
+constexpr uint32_t kPadOffset = 0x80000000u;
 
 // Largest row sum the fixed-max sweep accepts (see the header).
 template <typename T> constexpr float kFastLimit = 4294967296.0f;
@@ -171,8 +176,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
   // ---- tile staging straight into LDS: a padded tile is KSLOTS (VSLOTS)
   // 16-byte slots, slot s of a wave instruction landing at its base + 16*lane;
-  // the lane fetches the global chunk its slot holds (pad slots fetch an
-  // in-range chunk of the same row, which nobody reads)
+  // the lane fetches the global chunk its slot holds, and pad slots read out
+  // of range (zeros, no memory traffic; nobody reads them)
   constexpr int KSPR = KST / 8, VSPR = VST / 8;  // slots per padded row
   constexpr int KSLOTS = BN * KSPR, VSLOTS = BN * VSPR;
   constexpr int KI = (KSLOTS + NT - 1) / NT, VI = (VSLOTS + NT - 1) / NT;
@@ -180,12 +185,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
     const int sl = i * NT + tid, row = sl / KSPR, col = sl % KSPR;
-    kgo[i] = (row * (int)a.kss + (col < KCH ? col : col - (KSPR - KCH)) * 8) * (int)sizeof(T);
+    kgo[i] = col < KCH ? (row * (int)a.kss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
 #pragma unroll
   for (int i = 0; i < VI; ++i) {
     const int sl = i * NT + tid, row = sl / VSPR, col = sl % VSPR;
-    vgo[i] = (row * (int)a.vss + (col < KCH ? col : col - (VSPR - KCH)) * 8) * (int)sizeof(T);
+    vgo[i] = col < KCH ? (row * (int)a.vss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
   // dims 16kk + 8g ..), and the transposing V reads (see pv)
@@ -269,43 +274,69 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     l_i = 0.f;
   };
 
-  // ---- fast sweep: fixed max, S(t+1) pipelined with the softmax and PV of tile t
+  // ---- fast sweep: fixed max; each step exponentiates S(t), then runs the
+  // products of O += V(t)^T P(t)^T and S(t+1) over the same S registers
   clear();
   dma_k(0, 0);
   dma_v(0, 0);
   dma_k(1, 1);  // past the end this reads zeros or keys nobody uses
   landed();
   __syncthreads();
-  f32x16 sa = scores(0), sb;
-  if (need_mask(0)) apply_mask(0, sa);
+  f32x16 sc = scores(0);
+  if (need_mask(0)) apply_mask(0, sc);
   {
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[r]);
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[r]);
     m_i = fmaxf(mx, __shfl_xor(mx, 32, 64)) * a.c;
   }
   __syncthreads();  // K(0) is read; the first step overwrites its buffer
   Frag pf[2];
-  // Step t: S(t) in cur, S(t+1) into nxt. Buffers: K(t+1) in Ks[(t+1)&1] and
-  // V(t) in Vs[t&1] are read; K(t+2) goes to Ks[t&1] and V(t+1) to
-  // Vs[(t+1)&1], whose previous tiles were last read in step t-1.
-  auto step = [&](int t, f32x16& cur, f32x16& nxt) {
+  // Step t. Buffers: V(t) in Vs[t&1] and K(t+1) in Ks[(t+1)&1] are read;
+  // K(t+2) goes to Ks[t&1] and V(t+1) to Vs[(t+1)&1], whose previous tiles
+  // were last read in step t-1. Product i < KK is V^T P^T step i (16 keys c =
+  // i / DT, head dims 32 * (i % DT) ..); product KK + kk is S^T step kk.
+  // Fragment i + kRing is read as product i issues, and sched_barrier keeps
+  // that order (the compiler would otherwise bunch the reads).
+  auto step = [&](int t) {
     dma_k(min(t + 2, n_tiles), t & 1);
     dma_v(min(t + 1, n_tiles - 1), (t + 1) & 1);
-    if (need_mask(t)) apply_mask(t, cur);
-    nxt = scores((t + 1) & 1);
-    softmax(cur, m_i, pf);
-    pv(t & 1, pf);
+    if (need_mask(t)) apply_mask(t, sc);
+    softmax(sc, m_i, pf);
+    lds_s4* vt = (lds_s4*)(Vs[t & 1] + v_lane);
+    const T* ks = Ks[(t + 1) & 1] + k_lane;
+    auto fetch = [&](int i) -> Frag {
+      if (i < KK) {
+        const int c = i / DT, dt = i % DT;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
+        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+      return *reinterpret_cast<const Frag*>(ks + 16 * (i - KK));
+    };
+    constexpr int N = 2 * KK;  // 2 * DT == KK products of each kind
+    Frag ring[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) ring[i] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const Frag f = ring[i % kRing];
+      if (i + kRing < N) ring[i % kRing] = fetch(i + kRing);
+      if (i < KK) {
+        acc[i % DT] = Mma<T>::run(f, pf[i / DT], acc[i % DT]);
+      } else {
+        if (i == KK) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+        }
+        sc = Mma<T>::run(f, qf[i - KK], sc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     landed();
     __syncthreads();
   };
-  // pairs of steps keep each S in fixed registers; one exit keeps O in place
-  int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
-    step(t, sa, sb);
-    step(t + 1, sb, sa);
-  }
-  if (t < n_tiles) step(t, sa, sb);
+  for (int t = 0; t < n_tiles; ++t) step(t);
 
   {
     const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
