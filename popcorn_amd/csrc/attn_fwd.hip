@@ -40,17 +40,18 @@
 // when the max grows by more than 2^8), so the result never depends on the
 // data being benign. The log-sum-exp output is converted back to natural log.
 //
-// LDS layouts (a tile is contiguous 16-byte slots, padding included; a wave's
-// direct load fills 64 consecutive slots, and a lane whose slot is padding
-// reads past the buffer's range, which returns zeros without a memory access):
+// LDS layouts (a tile is contiguous 16-byte slots; a wave's direct load fills
+// 64 consecutive slots, each lane fetching the chunk its slot holds, and a
+// lane whose K slot is padding reads past the buffer's range, which returns
+// zeros without a memory access):
 //   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272
 //       (or 144) bytes apart and so cover all 64 banks once.
-//   V [BN][D + 32]: row-major, rows 64 bytes apart modulo 256. V^T fragments
-//       come from ds_read_b64_tr_b16: within a 16-lane group, lane s reads
-//       keys base + s/4, dims d0 + 4*(s%4) .. +3, and lane i receives dims
-//       d0 + i of keys base .. base + 3 -- half of one MFMA A fragment. The
-//       two 16-lane groups served together read 4 rows x 64 bytes, which the
-//       row offset spreads over all 64 banks.
+//   V [BN][D], unpadded, with chunk c of row r at slot c ^ vswz(r). V^T
+//       fragments come from ds_read_b64_tr_b16: within a 16-lane group, lane
+//       s reads keys base + s/4, dims d0 + 4*(s%4) .. +3, and lane i receives
+//       dims d0 + i of keys base .. base + 3 -- half of one MFMA A fragment.
+//       The two 16-lane groups served together read 4 rows x 4 chunks, which
+//       the swizzle places in 16 distinct slots of a 256-byte bank window.
 //
 // K and V are read through buffer resources based at the (batch, kv head):
 // a tile is one scalar offset, and rows at or past S read as zero, so no load
@@ -78,6 +79,11 @@ constexpr int kRing = 6;  // fragment reads in flight ahead of the product that 
 // (each below 2^31), and with a tile offset below 2^31 added it cannot wrap.
 constexpr uint32_t kPadOffset = 0x80000000u;
 
+// Slot of chunk c of V row r is c ^ vswz(r): the two 16-lane groups of a
+// transposing read cover 4 rows x 4 chunks, which this spreads over 16
+// distinct slots of a 256-byte bank window (rows of head_dim 64 are 128 bytes).
+template <int D> __device__ __forceinline__ int vswz(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+
 // Largest row sum the fixed-max sweep accepts (see the header).
 template <typename T> constexpr float kFastLimit = 4294967296.0f;
 template <> constexpr float kFastLimit<f16> = 32768.0f;
@@ -104,12 +110,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     AttnArgs a) {
   using Frag = typename Mma<T>::frag;
   constexpr int KST = D + 8;   // K row stride in LDS, elements
-  constexpr int VST = D + 32;  // V row stride in LDS, elements
   constexpr int KCH = D / 8;   // 16-byte chunks per K/V row
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
-  __shared__ __attribute__((aligned(16))) T Vs[2][BN * VST];
+  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
 
   // ---- work item: (batch, kv head, q tile) groups, q heads of a group adjacent on one XCD
   const int G = a.group;
@@ -174,28 +179,43 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  // ---- tile staging straight into LDS: a padded tile is KSLOTS (VSLOTS)
-  // 16-byte slots, slot s of a wave instruction landing at its base + 16*lane;
-  // the lane fetches the global chunk its slot holds, and pad slots read out
-  // of range (zeros, no memory traffic; nobody reads them)
-  constexpr int KSPR = KST / 8, VSPR = VST / 8;  // slots per padded row
-  constexpr int KSLOTS = BN * KSPR, VSLOTS = BN * VSPR;
-  constexpr int KI = (KSLOTS + NT - 1) / NT, VI = (VSLOTS + NT - 1) / NT;
-  int kgo[KI], vgo[VI];
+  // ---- tile staging straight into LDS: a padded K tile is KSLOTS 16-byte
+  // slots, slot s of a wave instruction landing at its base + 16*lane; the
+  // lane fetches the global chunk its slot holds, and pad slots read out of
+  // range (zeros, no memory traffic; nobody reads them)
+  constexpr int KSPR = KST / 8;  // slots per padded K row
+  constexpr int KSLOTS = BN * KSPR;
+  constexpr int KI = (KSLOTS + NT - 1) / NT;
+  int kgo[KI];
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
     const int sl = i * NT + tid, row = sl / KSPR, col = sl % KSPR;
     kgo[i] = col < KCH ? (row * (int)a.kss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
-#pragma unroll
-  for (int i = 0; i < VI; ++i) {
-    const int sl = i * NT + tid, row = sl / VSPR, col = sl % VSPR;
-    vgo[i] = col < KCH ? (row * (int)a.vss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
+  // V rows are unpadded, chunk c of row r at slot c ^ vswz(r); the rows of one
+  // instruction's slots differ from the next's by NT / KCH (a multiple of 4),
+  // so every instruction shares the lane's chunk and only the row base moves
+  constexpr int VI = BN * KCH / NT;
+  static_assert(BN * KCH % NT == 0 && (NT / KCH) % 4 == 0, "V staging covers whole rows");
+  int vgo;
+  {
+    const int row = tid / KCH, pos = tid % KCH;
+    vgo = (row * (int)a.vss + (pos ^ vswz<D>(row)) * 8) * (int)sizeof(T);
   }
   // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
   // dims 16kk + 8g ..), and the transposing V reads (see pv)
   const int k_lane = r32 * KST + 8 * g;
-  const int v_lane = (4 * g + ((lane & 15) >> 2)) * VST + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // V^T reads: the lane reads key row kr (+ 16c + 8h), dims 32 dt +
+  // 16 ((lane >> 4) & 1) + 4 (lane & 3) .. +3, i.e. chunk 4 dt + vq; with the
+  // swizzle that chunk sits at 4 (dt ^ vs) + vq, one offset per dt
+  int v_dt[DT];
+  {
+    const int kr = 4 * g + ((lane & 15) >> 2);
+    const int vq = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    const int vs = vswz<D>(kr) / 4;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) v_dt[dt] = kr * D + (4 * (dt ^ vs) + vq) * 8 + 4 * (lane & 1);
+  }
 
   // tile t of K into Ks[buf] / of V into Vs[buf], asynchronously (vmcnt)
   auto dma_k = [&](int t, int buf) {
@@ -209,8 +229,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     const int tile = t * BN * (int)a.vss * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < VI; ++i)
-      if (VSLOTS % NT == 0 || i * NT + tid < VSLOTS)
-        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
+      ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo, tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
   };
   auto landed = [&]() { lds_loads_landed(); };
   // S^T of the K tile in buffer buf
@@ -239,17 +258,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // transposing reads of row-major V: within each 16-lane group, lane s reads
   // keys (base + s/4), dims (d0 + 4*(s%4)) .. +3, and lane i receives dims
   // d0 + i of keys base .. base + 3.
+  auto vfrag = [&](const T* vb, int c, int dt) -> Frag {
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vb + v_dt[dt] + 16 * c * D));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(vb + v_dt[dt] + (16 * c + 8) * D));
+    return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
   auto pv = [&](int buf, const Frag (&pf)[2]) {
-    lds_s4* vt = (lds_s4*)(Vs[buf] + v_lane);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
-        acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf[c],
-                              acc[dt]);
-      }
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = Mma<T>::run(vfrag(Vs[buf], c, dt), pf[c], acc[dt]);
   };
   float m_i;  // reference max of s * c for query q_row
   float l_i;  // this lane's half of the denominator
@@ -303,15 +321,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     dma_v(min(t + 1, n_tiles - 1), (t + 1) & 1);
     if (need_mask(t)) apply_mask(t, sc);
     softmax(sc, m_i, pf);
-    lds_s4* vt = (lds_s4*)(Vs[t & 1] + v_lane);
     const T* ks = Ks[(t + 1) & 1] + k_lane;
     auto fetch = [&](int i) -> Frag {
-      if (i < KK) {
-        const int c = i / DT, dt = i % DT;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c) * VST + dt * 32) / 4);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt + ((16 * c + 8) * VST + dt * 32) / 4);
-        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
+      if (i < KK) return vfrag(Vs[t & 1], i / DT, i % DT);
       return *reinterpret_cast<const Frag*>(ks + 16 * (i - KK));
     };
     constexpr int N = 2 * KK;  // 2 * DT == KK products of each kind
