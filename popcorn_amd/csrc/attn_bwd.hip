@@ -55,6 +55,8 @@ constexpr int BM = 128;  // dq kernel: query rows per block
 constexpr int BN = 32;   // dq kernel: keys per tile
 constexpr int BK = 128;  // dkdv kernel: keys per block
 constexpr int BQ = 32;   // dkdv kernel: query rows per tile
+constexpr int kRingDq = 3;    // dq kernel: fragment reads in flight ahead of their product
+constexpr int kRingDkdv = 4;  // dkdv kernel: the same
 
 struct BwdArgs {
   const void *q, *k, *v, *o, *dout;
@@ -229,13 +231,33 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     if (!(CAUSAL && kv0 > wave_first + 31)) {
       const T* ks = Ks[buf];
       const T* vs = Vs[buf];
+      // 2 KK score products (S^T from K, dP^T from V, alternating), then DT x 2
+      // products of dQ^T; fragment reads run kRingDq products ahead, and
+      // sched_barrier keeps that order
+      constexpr int RING = kRingDq;
+      constexpr int NSC = 2 * KK, NALL = 3 * KK;
+      auto fetch = [&](int i) -> Frag {
+        if (i < NSC) return *reinterpret_cast<const Frag*>((i & 1 ? vs : ks) + a_lane[i / 2]);
+        const int u = i - NSC, c = u / DT, dt = u % DT;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[0][dt] + 16 * c * L::ST));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[1][dt] + 16 * c * L::ST));
+        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      Frag ring[RING];
+#pragma unroll
+      for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        s = Mma<T>::run(*reinterpret_cast<const Frag*>(ks + a_lane[kk]), qf[kk], s);
-        dp = Mma<T>::run(*reinterpret_cast<const Frag*>(vs + a_lane[kk]), gf[kk], dp);
+      for (int i = 0; i < NSC; ++i) {
+        const Frag f = ring[i % RING];
+        ring[i % RING] = fetch(i + RING);
+        if (i & 1)
+          dp = Mma<T>::run(f, gf[i / 2], dp);
+        else
+          s = Mma<T>::run(f, qf[i / 2], s);
+        __builtin_amdgcn_sched_barrier(0);
       }
       const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > S;
       const int lim = CAUSAL ? min(q_row, S - 1) : S - 1;
@@ -249,16 +271,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
           if (need_mask) p = kv0 + 8 * (r >> 2) + 4 * g + (r & 3) <= lim ? p : 0.f;
           dsf[c][j] = (T)(p * (dp[r] - dsum));
         }
+      __builtin_amdgcn_sched_barrier(0);
       // dQ^T += K^T dS^T: K^T fragments from transposing reads of the K tile
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[0][dt] + 16 * c * L::ST));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[1][dt] + 16 * c * L::ST));
-          acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
-                                dsf[c], acc[dt]);
-        }
+      for (int i = NSC; i < NALL; ++i) {
+        const Frag f = ring[i % RING];
+        if (i + RING < NALL) ring[i % RING] = fetch(i + RING);
+        const int u = i - NSC;
+        acc[u % DT] = Mma<T>::run(f, dsf[u / DT], acc[u % DT]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     lds_loads_landed();
     __syncthreads();
@@ -396,28 +418,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  // 16 x 32 score block of the tile in stage st against this slice's keys,
-  // A operand from `base` (Q for role 0, dO for role 1)
-  auto product = [&](const T* base) {
-    f32x16 s;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) s = Mma<T>::run(*reinterpret_cast<const Frag*>(base + a_lane[kk]), bf[kk], s);
-    return s;
-  };
-  // acc^T += X^T F with X^T fragments from transposing reads of the tile at `base`
-  auto accumulate = [&](const T* base, const Frag (&f)[2]) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + t_lane[0][dt] + 16 * c * L::ST));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + t_lane[1][dt] + 16 * c * L::ST));
-        acc[dt] = Mma<T>::run(__builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), f[c],
-                              acc[dt]);
-      }
-  };
   // this lane's 16 values of a tile's row vector v (rows 8j + 4g + i, r = 4j + i)
   auto rows16 = [&](const float* v, float (&out)[16]) {
 #pragma unroll
@@ -440,43 +440,80 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   loads_landed_but<(NS - 3) * PER_ISSUE>();
   __syncthreads();
   (void)pmine;
+  // One step's 16 products: 8 of the score block (A from the tile at `pbase`,
+  // B = the lane's key row) then 8 of the accumulation (A^T from transposing
+  // reads of the tile at `abase`, B from `mid`, which turns the score block
+  // into the B fragments between the two halves). Fragment reads run
+  // kRingDkdv products ahead, across the two halves.
+  constexpr int RING = kRingDkdv;
+  auto run16 = [&](const T* pbase, const T* abase, auto mid) {
+    auto fetch = [&](int i) -> Frag {
+      if (i < KK) return *reinterpret_cast<const Frag*>(pbase + a_lane[i]);
+      const int u = i - KK, c = u / DT, dt = u % DT;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[0][dt] + 16 * c * L::ST));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[1][dt] + 16 * c * L::ST));
+      return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    Frag ring[RING];
+#pragma unroll
+    for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
+    f32x16 sres;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sres[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < KK; ++i) {
+      const Frag f = ring[i % RING];
+      ring[i % RING] = fetch(i + RING);
+      sres = Mma<T>::run(f, bf[i], sres);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    Frag bfr[2];
+    mid(sres, bfr);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = KK; i < 2 * KK; ++i) {
+      const Frag f = ring[i % RING];
+      if (i + RING < 2 * KK) ring[i % RING] = fetch(i + RING);
+      const int u = i - KK;
+      acc[u % DT] = Mma<T>::run(f, bfr[u / DT], acc[u % DT]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
   for (int t = 0; t <= n_it; ++t) {
     issue(t + NS - 2, (t + NS - 2) % NS);
     if (role == 0) {
       if (t < n_it) {
         const int st = t % NS;
         const T* qs = QG[st];
-        const f32x16 s = product(qs);
         const int q0 = (u0 + t % n_u) * BQ;
         float l2[16];
         rows16(RV[st][0], l2);
         // tiles wholly before this slice's keys (causal) are masked to zero, not skipped
         const bool need_mask = (CAUSAL && q0 < kw0 + 32) || !key_ok || q0 + BQ > S;
-        float p[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], cs, -l2[r]));
-          if (need_mask) {
-            const int qrow = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
-            p[r] = key_ok && qrow < S && (!CAUSAL || key <= qrow) ? p[r] : 0.f;
-          }
-        }
         float* pw = Pb[t & 1][slice];
+        run16(qs, qs + TILE, [&](const f32x16& s, Frag (&pf)[2]) {
+          float p[16];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          *reinterpret_cast<float4*>(pw + 256 * j + 4 * lane) = make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
-        Frag pf[2];
+          for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], cs, -l2[r]));
+            if (need_mask) {
+              const int qrow = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+              p[r] = key_ok && qrow < S && (!CAUSAL || key <= qrow) ? p[r] : 0.f;
+            }
+          }
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<float4*>(pw + 256 * j + 4 * lane) = make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pf[c][j] = (T)p[8 * c + j];
-        accumulate(qs + TILE, pf);  // dV^T += dO^T P
+          for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pf[c][j] = (T)p[8 * c + j];
+        });  // dV^T += dO^T P
       }
     } else if (t > 0) {
       const int u = t - 1;
       const int st = u % NS;
       const T* qs = QG[st];
-      const f32x16 dp = product(qs + TILE);
       float dd[16], p[16];
       rows16(RV[st][1], dd);
       const float* pr = Pb[u & 1][slice];
@@ -488,12 +525,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
         p[4 * j + 2] = x.z;
         p[4 * j + 3] = x.w;
       }
-      Frag dsf[2];
+      run16(qs + TILE, qs, [&](const f32x16& dp, Frag (&dsf)[2]) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dsf[c][j] = (T)(p[8 * c + j] * (dp[8 * c + j] - dd[8 * c + j]));
-      accumulate(qs, dsf);  // dK^T += Q^T dS
+          for (int j = 0; j < 8; ++j) dsf[c][j] = (T)(p[8 * c + j] * (dp[8 * c + j] - dd[8 * c + j]));
+      });  // dK^T += Q^T dS
     }
     loads_landed_but<(NS - 3) * PER_ISSUE>();
     __syncthreads();
