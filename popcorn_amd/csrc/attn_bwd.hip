@@ -378,29 +378,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
     const int row = within / KCH, c = (within % KCH) ^ L::swz(row);
     go[i] = (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T);
   }
-  // tile `it` (clamped: past the end it reloads the last tile) into stage st
-  auto issue = [&](int it, int st) {
-    const int itc = min(it, n_it - 1);
-    const int hq = hkv * a.group + itc / n_u;
-    const int r0 = (u0 + itc % n_u) * BQ;
+  // Tiles are issued in order: a cursor holds the next tile's q head (within
+  // the group) and q tile, and the buffer descriptors of that head, rebuilt
+  // only when the head changes; past the end the last tile is issued again.
+  // Rows past the end read as zero; their p is masked. Wave 0 also loads the
+  // rows' lse2, wave 1 their D, the other waves repeat D into `spill`.
+  int cur_h = 0, cur_u = 0, cur_it = 0;
+  __amdgpu_buffer_rsrc_t trs[TI], rrs;
+  int tstride[TI];  // bytes per row of the tensor each of this wave's tile loads reads
+  auto set_head = [&](int h) {
+    const int hq = hkv * a.group + h;
     const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const T* gb = static_cast<const T*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
     const float* db = a.dsum + b * a.lse_bs + hq * a.lse_hs + start;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
-      const int first = i * NT2 + wave * 64;  // wave-uniform
-      const bool isq = first < SLOTS;
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(isq ? qb : gb), (short)0,
-          (int)(((int64_t)(S - 1) * (isq ? a.qs[1] : a.gs[1]) + D) * (int)sizeof(T)), 0x00020000);
-      ld_buf_lds(rs, QG[st] + first * 8, go[i], r0 * (int)(isq ? a.qs[1] : a.gs[1]) * (int)sizeof(T));
+      const bool isq = i * NT2 + wave * 64 < SLOTS;  // wave-uniform
+      tstride[i] = (int)(isq ? a.qs[1] : a.gs[1]) * (int)sizeof(T);
+      trs[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(isq ? qb : gb), (short)0,
+                                                 (int)(((int64_t)(S - 1) * (isq ? a.qs[1] : a.gs[1]) + D) * (int)sizeof(T)),
+                                                 0x00020000);
     }
-    // rows past the end read as zero; their p is masked. wave 0: lse2 of the
-    // rows; wave 1: D; the other waves repeat D into `spill`
-    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(wave == 0 ? db + a.lse_n : db), (short)0, S * (int)sizeof(float), 0x00020000);
+    rrs = __builtin_amdgcn_make_buffer_rsrc((void*)(wave == 0 ? db + a.lse_n : db), (short)0, S * (int)sizeof(float),
+                                            0x00020000);
+  };
+  set_head(0);
+  // the cursor's tile into stage st, then advance the cursor
+  auto issue = [&](int st) {
+    const int r0 = (u0 + cur_u) * BQ;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) ld_buf_lds(trs[i], QG[st] + (i * NT2 + wave * 64) * 8, go[i], r0 * tstride[i]);
     ld_buf_lds4(rrs, wave == 0 ? RV[st][0] : (wave == 1 ? RV[st][1] : spill), lane * (int)sizeof(float),
                 r0 * (int)sizeof(float));
+    if (cur_it + 1 < n_it) {
+      ++cur_it;
+      if (++cur_u == n_u) {
+        cur_u = 0;
+        set_head(++cur_h);
+      }
+    }
   };
 
   int a_lane[KK], t_lane[2][DT];
@@ -436,7 +452,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   // Pb[(t - 1) & 1]). Tile t + NS - 2 is issued into the stage of tile t - 2,
   // which role 1 finished in step t - 1; the step ends once tile t + 1 has landed.
 #pragma unroll
-  for (int j = 0; j < NS - 2; ++j) issue(j, j);
+  for (int j = 0; j < NS - 2; ++j) issue(j);
   loads_landed_but<(NS - 3) * PER_ISSUE>();
   __syncthreads();
   (void)pmine;
@@ -480,7 +496,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
     }
   };
   for (int t = 0; t <= n_it; ++t) {
-    issue(t + NS - 2, (t + NS - 2) % NS);
+    issue((t + NS - 2) % NS);
     if (role == 0) {
       if (t < n_it) {
         const int st = t % NS;
