@@ -1,9 +1,12 @@
 // Attention forward (flash-style, grouped-query, optional causal mask) on
 // gfx950 matrix cores.
 //
-// Block = 4 wavefronts x 32 query rows (BM = 128) of one (batch, q head);
-// three blocks share a CU (three waves per SIMD). Keys stream through LDS in
-// tiles of BN = 32.
+// Block = 4 wavefronts of 32 query rows each, over one (batch, kv head):
+// gp q heads of that kv head's group (4, 2 or 1, the largest dividing the
+// group size) x 4/gp consecutive row groups. With 4 q heads per kv head every
+// wave holds the same 32 rows of its own head, so the block's K/V tiles serve
+// all four and every wave sees the same causal range. Three blocks share a CU
+// (three waves per SIMD). Keys stream through LDS in tiles of BN = 32.
 //
 // Per tile each wave computes
 //   S^T (32 keys x 32 queries)  = K_tile . Q^T   (v_mfma_f32_32x32x16, K from
@@ -56,9 +59,8 @@
 // K and V are read through buffer resources based at the (batch, kv head):
 // a tile is one scalar offset, and rows at or past S read as zero, so no load
 // is predicated; such keys are masked like causal ones. Work order: longest
-// causal rows first, and the q heads sharing a kv head land on the same XCD
-// (dispatch is round-robin over the 8 XCDs), so their K/V tiles are shared
-// through that XCD's L2.
+// causal rows first; the q tiles of one (batch, kv head) land on the same XCD
+// (dispatch is round-robin over the 8 XCDs) and read the same K/V prefix.
 #include <math.h>
 
 #include <type_traits>
@@ -71,7 +73,6 @@ namespace {
 
 using namespace attn;
 
-constexpr int BM = 128;
 constexpr int BN = 32;
 constexpr int NT = 256;
 constexpr int kRing = 6;  // fragment reads in flight ahead of the product that uses them
@@ -101,6 +102,7 @@ struct AttnArgs {
   int64_t qsb, qss, qsh, ksb, kss, ksh, vsb, vss, vsh, osb, oss, osh;
   int64_t lse_bs, lse_hs;  // lse element (b, h, token t of b) at b*lse_bs + h*lse_hs + t (+ cu[b] when packed)
   int B, S, Hq, Hkv, group, m_tiles;
+  int gp;  // q heads of one kv group per block (4, 2 or 1); the block's 4 waves are gp heads x 4/gp row groups
   float c;          // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
 };
@@ -116,24 +118,24 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
   __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
 
-  // ---- work item: (batch, kv head, q tile) groups, q heads of a group adjacent on one XCD
-  const int G = a.group;
+  // ---- work item: (q tile, batch, kv head, head quad), longest causal rows
+  // first. A block's waves are gp q heads of one kv group x 4/gp row groups of
+  // 32, so its K/V tiles serve every head it holds; with B * Hkv * G/gp a
+  // multiple of 8, all q tiles of one (batch, kv head, quad) land on one XCD
+  // (dispatch is round-robin over the 8 XCDs), where they read the same K/V
+  // prefix at about the same time.
+  const int G = a.group, GP = a.gp;
+  const int n_quads = G / GP;
+  const int per_tile = a.B * a.Hkv * n_quads;
   const int w = blockIdx.x;
-  int gidx, hig;
-  if (gridDim.x % (8 * G) == 0) {
-    const int wp = w >> 3;
-    gidx = (wp / G) * 8 + (w & 7);
-    hig = wp % G;
-  } else {
-    gidx = w / G;
-    hig = w % G;
-  }
-  const int per_tile = a.B * a.Hkv;
-  const int m_tile = a.m_tiles - 1 - gidx / per_tile;
-  const int rest = gidx % per_tile;
-  const int b = rest / a.Hkv;
-  const int hkv = rest % a.Hkv;
-  const int hq = hkv * G + hig;
+  const int m_tile = a.m_tiles - 1 - w / per_tile;
+  const int rest = w % per_tile;
+  const int b = rest / (a.Hkv * n_quads);
+  const int hkv = (rest / n_quads) % a.Hkv;
+  const int quad = rest % n_quads;
+  const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hq = hkv * G + quad * GP + wave_id % GP;
+  const int rows_per_block = 32 * (4 / GP);
 
   // this block's sequence: all of it for a dense batch; tokens [cu[b], cu[b+1])
   // of a packed one (clamped, so a malformed table cannot address past `total`)
@@ -142,7 +144,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     start = min(max(a.cu[b], 0), a.total);
     S = min(min(max(a.cu[b + 1], start), a.total) - start, a.S);
   }
-  const int m0 = m_tile * BM;
+  const int m0 = m_tile * rows_per_block;
   if (m0 >= S) return;  // whole block: before any barrier
 
   const int tid = threadIdx.x;
@@ -150,7 +152,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int lane = tid & 63;
   const int r32 = lane & 31;
   const int g = lane >> 5;
-  const int wave_first = m0 + wave * 32;
+  const int wave_first = m0 + (wave / GP) * 32;
   const int q_row = wave_first + r32;
 
   const T* qbase = static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh + start * a.qss;
@@ -176,7 +178,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     qf[kk] = __builtin_bit_cast(Frag, raw);
   }
 
-  const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
+  const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
   // ---- tile staging straight into LDS: a padded K tile is KSLOTS 16-byte
@@ -413,7 +415,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 template <typename T, int D>
 int launch(const AttnArgs& a, bool causal, hipStream_t s) {
-  const int64_t blocks = (int64_t)a.m_tiles * a.B * a.Hq;
+  const int64_t blocks = (int64_t)a.m_tiles * a.B * a.Hq / a.gp;
   if (causal)
     hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3(blocks), dim3(NT), 0, s, a);
   else
@@ -467,7 +469,8 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   a.Hq = (int)q_heads;
   a.Hkv = (int)kv_heads;
   a.group = (int)(q_heads / kv_heads);
-  a.m_tiles = (int)((seq + BM - 1) / BM);
+  a.gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
+  a.m_tiles = (int)((seq + 32 * (4 / a.gp) - 1) / (32 * (4 / a.gp)));
   // Buffer offsets are 32-bit: within one sequence the tile loads reach up to
   // two tiles past its last row (reading zeros there), and every such offset
   // must fit.
@@ -475,7 +478,7 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   if (reach > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: K/V rows span more than 2 GiB per head", who);
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
-  if ((int64_t)a.m_tiles * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
+  if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == PK_BF16) return head_dim == 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
   return head_dim == 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
