@@ -52,6 +52,16 @@ def test_attn_groups_and_scale(hkv, scale):
     _check(1, 96, 8, hkv, 128, True, scale, torch.bfloat16, seed=3)
 
 
+@pytest.mark.parametrize("heads", [(6, 2), (6, 1), (12, 2), (2, 1)], ids=str)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_attn_uneven_group_sizes(heads, causal, d):
+    """Group sizes 3, 6, 6 and 2: a block holds one or two q heads of a group over several
+    32-row groups (four heads per block only when 4 divides the group size)."""
+    hq, hkv = heads
+    _check(2, 200, hq, hkv, d, causal, None, torch.bfloat16, seed=7)
+
+
 def test_attn_popcorn_smoke_case():
     """The case Popcorn's per-backend smoke runs for attn (tests/kernels/test_kernels.py:107-123)."""
     _check(2, 64, 8, 2, 64, True, None, torch.bfloat16, seed=5)

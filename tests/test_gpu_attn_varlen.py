@@ -52,6 +52,12 @@ def test_attn_varlen_groups_and_scale(hkv, scale):
     _check(700, 5, 8, hkv, 128, True, scale, torch.bfloat16, seed=4)
 
 
+@pytest.mark.parametrize("heads", [(6, 2), (12, 2)], ids=str)
+def test_attn_varlen_uneven_group_sizes(heads):
+    """Group sizes 3 and 6 over packed segments of unequal lengths."""
+    _check(700, 5, heads[0], heads[1], 64, True, None, torch.bfloat16, seed=6)
+
+
 def test_attn_varlen_equal_segments_match_the_dense_kernel():
     """B sequences of one length packed back to back give the dense kernel's result bit for bit."""
     b, s, hq, hkv, d = 3, 333, 8, 2, 128
