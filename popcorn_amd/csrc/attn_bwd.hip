@@ -2,9 +2,10 @@
 // packed sequences) on gfx950 matrix cores, in two deterministic kernels
 // that never add into shared memory of another block:
 //
-//   dq kernel   one block = 4 waves x 32 query rows of one (sequence, q head),
-//               keys streamed through LDS in tiles of 32. Per tile each wave
-//               recomputes S^T = K Q^T and dP^T = V dO^T, forms
+//   dq kernel   one block = 4 waves x 32 query rows over one (sequence, kv
+//               head): gp of its q heads x 4/gp row groups, as in the
+//               forward; keys streamed through LDS in tiles of 32. Per tile
+//               each wave recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //               P = exp2(s*c - lse2) from the forward's log-sum-exp and
 //               dS = P (dP - D), and accumulates dQ^T += K^T dS^T. Its prologue
 //               also computes D = rowsum(dO * O) for its rows and stores it,
@@ -51,7 +52,7 @@ namespace {
 using namespace attn;
 
 constexpr int NT = 256;
-constexpr int BM = 128;  // dq kernel: query rows per block
+constexpr int BM = 128;  // dq kernel: query rows per block times q heads per block
 constexpr int BN = 32;   // dq kernel: keys per tile
 constexpr int BK = 128;  // dkdv kernel: keys per block
 constexpr int BQ = 32;   // dkdv kernel: query rows per tile
@@ -114,29 +115,25 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * L::ST];
   __shared__ __attribute__((aligned(16))) T Vs[2][BN * L::ST];
 
-  // work item: (q tile, batch, kv head) groups, longest causal rows first; the
-  // q heads of a group are adjacent on one XCD (dispatch is round-robin over
-  // the 8 XCDs), so their shared K/V tiles are fetched into that XCD's L2 once
-  const int m_tiles = (a.S + BM - 1) / BM;
+  // work item: (q tile, batch, kv head, head quad), longest causal rows
+  // first; the waves are gp q heads of one kv group (gp = 4, 2 or 1, the
+  // largest dividing the group size) x 4/gp row groups of 32, so with a group
+  // of 4 every wave covers the same rows and the same keys
   const int G = a.group;
+  const int GP = G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1);
+  const int rows_per_block = 32 * (4 / GP);
+  const int m_tiles = (a.S + rows_per_block - 1) / rows_per_block;
+  const int n_quads = G / GP;
+  const int per_tile = a.B * a.Hkv * n_quads;
   const int w = blockIdx.x;
-  int gidx, hig;
-  if (gridDim.x % (8 * G) == 0) {
-    const int wp = w >> 3;
-    gidx = (wp / G) * 8 + (w & 7);
-    hig = wp % G;
-  } else {
-    gidx = w / G;
-    hig = w % G;
-  }
-  const int per_tile = a.B * a.Hkv;
-  const int m_tile = m_tiles - 1 - gidx / per_tile;
-  const int b = (gidx % per_tile) / a.Hkv;
-  const int hkv = gidx % a.Hkv;
-  const int hq = hkv * G + hig;
+  const int m_tile = m_tiles - 1 - w / per_tile;
+  const int rest = w % per_tile;
+  const int b = rest / (a.Hkv * n_quads);
+  const int hkv = (rest / n_quads) % a.Hkv;
+  const int hq = hkv * G + (rest % n_quads) * GP + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % GP;
   int start, S;
   seq_bounds(a, b, start, S);
-  const int m0 = m_tile * BM;
+  const int m0 = m_tile * rows_per_block;
   if (m0 >= S) return;  // whole block, before any barrier
 
   const int tid = threadIdx.x;
@@ -144,7 +141,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int lane = tid & 63;
   const int r32 = lane & 31;
   const int g = lane >> 5;
-  const int wave_first = m0 + wave * 32;
+  const int wave_first = m0 + (wave / GP) * 32;
   const int q_row = wave_first + r32;
   const bool row_ok = q_row < S;
 
@@ -185,7 +182,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     a.dsum[a.lse_n + lidx] = lse2;
   }
 
-  const int kv_end = CAUSAL ? min(m0 + BM, S) : S;
+  const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
   // staging straight into LDS: slot i*NT + tid of a tile is row sl / KCH,
@@ -569,7 +566,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 
 template <typename T, int D>
 int launch(const BwdArgs& a, bool causal, hipStream_t s) {
-  const int64_t dq_blocks = (int64_t)((a.S + BM - 1) / BM) * a.B * a.Hq;
+  const int gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
+  const int64_t dq_blocks = (int64_t)((a.S + 32 * (4 / gp) - 1) / (32 * (4 / gp))) * a.B * a.Hq / gp;
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv;
   if (causal) {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true>), dim3(dq_blocks), dim3(NT), 0, s, a);

@@ -54,6 +54,13 @@ def test_attn_bwd_shapes(seq, causal, d, dtype):
     _check(2, seq, 8, 2, d, causal, None, dtype)
 
 
+@pytest.mark.parametrize("heads", [(6, 2), (6, 1), (12, 2)], ids=str)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_attn_bwd_uneven_group_sizes(heads, causal):
+    """Group sizes 3 and 6: the dq kernel's blocks hold one or two q heads over several row groups."""
+    _check(2, 150, heads[0], heads[1], 64, causal, None, torch.bfloat16, seed=11)
+
+
 @pytest.mark.parametrize("hkv", [8, 4, 1])
 @pytest.mark.parametrize("scale", [None, 0.25])
 def test_attn_bwd_groups_and_scale(hkv, scale):
