@@ -401,7 +401,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
         o, lse = impls.attn_with_lse(q, k, v, True)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=dev)
+        ws = torch.empty(lib.pk_attn_bwd_workspace(B, S, HQ, HKV, D), dtype=torch.uint8, device=dev)
         strides = (_lib._i64 * 24)(*(s for t in (q, k, v, o, do, dq, dk, dv) for s in t.stride()[:3]))
 
         def step(i):
@@ -410,7 +410,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
 
         def launch(i):
             _lib.check(lib.pk_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
-                                       lse.data_ptr(), dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                       lse.data_ptr(), ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(),
+                                       dv.data_ptr(),
                                        strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
 
         def cpu():

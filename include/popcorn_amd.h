@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 2
+#define PK_ABI_VERSION 3
 
 /* status codes */
 #define PK_OK 0
@@ -212,31 +212,52 @@ int pk_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o, flo
                        int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
 
 /*
+ * Bytes of device workspace pk_attn_bwd needs for this shape on the current
+ * device, or -1 for an invalid shape. It holds D = rowsum(dout * o) and
+ * lse * log2(e) (twice lse's size in fp32), and, when the dk/dv grid would
+ * leave CUs idle (small batches or short sequences), fp32 dk/dv partials of
+ * the q-head splits [splits, 2, batch * seq, kv_heads, head_dim].
+ * No counterpart in the reference (its backward is torch autograd).
+ */
+int64_t pk_attn_bwd_workspace(int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim);
+
+/*
  * Attention backward for pk_attn_fwd: given o, the upstream gradient dout
  * (like o) and the forward's lse, writes dq (like q), dk and dv (like k, v).
- * dsum is caller scratch of twice lse's size (fp32 [2, batch, q_heads, seq]);
- * it receives D = rowsum(dout * o), then lse * log2(e). Arithmetic: P is recomputed from q, k and
- * lse; dS = P (dP - D); dq = scale dS k, dk = scale dS^T q (summed over the q
- * heads of each kv head), dv = P^T dout; fp32 accumulation, one rounding per
- * output, no atomics (the result is deterministic). strides[24] = q, k, v, o,
- * dout, dq, dk, dv (batch, token, head) strides in elements.
+ * workspace: 16-byte aligned device memory of at least
+ * pk_attn_bwd_workspace() bytes (workspace_bytes says how many were given).
+ * Arithmetic: P is recomputed from q, k and lse; dS = P (dP - D);
+ * dq = scale dS k, dk = scale dS^T q (summed over the q heads of each kv
+ * head), dv = P^T dout; fp32 accumulation, one rounding per output, no atomics
+ * (partials of q-head splits are added in a fixed order, so the result is
+ * deterministic). strides[24] = q, k, v, o, dout, dq, dk, dv (batch, token,
+ * head) strides in elements.
  * Replaces torch autograd of the reference `attn` (kernels/attn.py:30-37).
  */
 int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
-                float* dsum, void* dq, void* dk, void* dv, const int64_t* strides, int64_t batch, int64_t seq,
-                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype,
-                void* stream);
+                void* workspace, int64_t workspace_bytes, void* dq, void* dk, void* dv, const int64_t* strides,
+                int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
+                int causal, int dtype, void* stream);
+
+/*
+ * Workspace bytes of pk_attn_varlen_bwd (as pk_attn_bwd_workspace, with
+ * total packed tokens in place of batch * seq), or -1 for an invalid shape.
+ * No counterpart in the reference.
+ */
+int64_t pk_attn_varlen_bwd_workspace(int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                                     int64_t kv_heads, int64_t head_dim);
 
 /*
  * Backward of pk_attn_varlen_fwd (packed sequences). lse is fp32
- * [q_heads, total] and dsum fp32 [2, q_heads, total]; strides[16] = q, k, v, o, dout, dq, dk, dv (token, head).
- * Replaces torch autograd of the reference `attn_varlen`
+ * [q_heads, total]; workspace as for pk_attn_bwd, sized by
+ * pk_attn_varlen_bwd_workspace(); strides[16] = q, k, v, o, dout, dq, dk, dv
+ * (token, head). Replaces torch autograd of the reference `attn_varlen`
  * (kernels/attn_varlen.py:41-54).
  */
 int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
-                       float* dsum, void* dq, void* dk, void* dv, const int* cu_seqlens, const int64_t* strides,
-                       int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads, int64_t kv_heads,
-                       int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
+                       void* workspace, int64_t workspace_bytes, void* dq, void* dk, void* dv, const int* cu_seqlens,
+                       const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,13 @@ struct BwdArgs {
   int64_t qs[3], ks[3], vs[3], os[3], gs[3], dqs[3], dks[3], dvs[3];  // (batch, token, head) strides
   int64_t lse_bs, lse_hs;
   int64_t lse_n;  // elements of lse; dsum[lse_n + i] holds lse[i] * log2(e)
+  // dk/dv head split: nsplit > 1 blocks per (key tile, kv head), each over
+  // group / nsplit of its q heads, leave fp32 partials in part
+  // [nsplit][2 (dV, dK)][rows][Hkv][D] (rows: batch * S tokens, or total when
+  // packed), summed in split order by dkdv_sum_kernel
+  float* part;
+  int nsplit;
+  int64_t rows;
   int B, S, Hq, Hkv, group;
   float scale;  // signed softmax scale
   float c;      // |scale| * log2(e), at least 1e-30
@@ -320,10 +327,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) float Pb[2][4][16 * 64];
 
   const int w = blockIdx.x;
-  const int per_tile = a.B * a.Hkv;
+  const int per_tile = a.B * a.Hkv * a.nsplit;
   const int kv_tile = w / per_tile;  // first key tiles (the most causal work) first
-  const int b = (w % per_tile) / a.Hkv;
-  const int hkv = w % a.Hkv;
+  const int b = (w % per_tile) / (a.Hkv * a.nsplit);
+  const int hkv = (w / a.nsplit) % a.Hkv;
+  const int split = w % a.nsplit;
+  const int heads = a.group / a.nsplit;  // q heads this block walks, from split * heads on
   int start, S;
   seq_bounds(a, b, start, S);
   const int kb0 = kv_tile * BK;
@@ -363,7 +372,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   // query tiles: every q head of the group, rows from the block's first key on (causal)
   const int u0 = CAUSAL ? kb0 / BQ : 0;
   const int n_u = (S + BQ - 1) / BQ - u0;
-  const int n_it = a.group * n_u;
+  const int n_it = heads * n_u;
 
   // staging: slot sl = i*NT2 + tid of the stage (Q slots, then dO slots) is
   // row (sl % SLOTS) / KCH of that tile, stored chunk sl % KCH, which holds
@@ -384,7 +393,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   __amdgpu_buffer_rsrc_t trs[TI], rrs;
   int tstride[TI];  // bytes per row of the tensor each of this wave's tile loads reads
   auto set_head = [&](int h) {
-    const int hq = hkv * a.group + h;
+    const int hq = hkv * a.group + split * heads + h;
     const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const T* gb = static_cast<const T*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
     const float* db = a.dsum + b * a.lse_bs + hq * a.lse_hs + start;
@@ -551,16 +560,59 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   loads_landed_but<0>();  // tiles issued past the end, before the block's LDS is released
 
   if (key_ok) {
-    T* out = role == 0
-                 ? static_cast<T*>(a.dv) + b * a.dvs[0] + hkv * a.dvs[2] + (int64_t)(start + key) * a.dvs[1]
-                 : static_cast<T*>(a.dk) + b * a.dks[0] + hkv * a.dks[2] + (int64_t)(start + key) * a.dks[1];
     const float f = role == 0 ? 1.0f : a.scale;  // dK: signed scale, Q was staged unflipped
+    if (a.nsplit > 1) {
+      // fp32 partial of this block's heads; dkdv_sum_kernel adds the splits
+      const int64_t row = (a.cu != nullptr ? (int64_t)start : (int64_t)b * a.S) + key;
+      float* out = a.part + (((int64_t)(split * 2 + role) * a.rows + row) * a.Hkv + hkv) * D;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq)
-        *reinterpret_cast<uint2*>(out + dt * 32 + 8 * rq + 4 * g) =
-            pack4<T>(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
+        for (int rq = 0; rq < 4; ++rq)
+          *reinterpret_cast<float4*>(out + dt * 32 + 8 * rq + 4 * g) =
+              make_float4(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
+    } else {
+      T* out = role == 0
+                   ? static_cast<T*>(a.dv) + b * a.dvs[0] + hkv * a.dvs[2] + (int64_t)(start + key) * a.dvs[1]
+                   : static_cast<T*>(a.dk) + b * a.dks[0] + hkv * a.dks[2] + (int64_t)(start + key) * a.dks[1];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+          *reinterpret_cast<uint2*>(out + dt * 32 + 8 * rq + 4 * g) =
+              pack4<T>(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
+    }
+  }
+}
+
+// dV (role 0) and dK (role 1) of one token row, kv head and 4 dims: the sum of
+// the nsplit partials in split order, rounded once. Rows are batch * S tokens
+// (dense) or the packed token index.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dkdv_sum_kernel(BwdArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over rows * Hkv * D / 4
+  const int64_t n = a.rows * a.Hkv * (D / 4);
+  if (i >= n) return;
+  const int d4 = (int)(i % (D / 4)) * 4;
+  const int hkv = (int)((i / (D / 4)) % a.Hkv);
+  const int64_t row = i / ((int64_t)(D / 4) * a.Hkv);
+  const int64_t b = a.cu != nullptr ? 0 : row / a.S;
+  const int64_t t = a.cu != nullptr ? row : row % a.S;
+  const int64_t stride = a.rows * a.Hkv * D;  // one (split, role) slab
+#pragma unroll
+  for (int role = 0; role < 2; ++role) {
+    const float* p = a.part + (int64_t)role * stride + (row * a.Hkv + hkv) * D + d4;
+    float4 s = *reinterpret_cast<const float4*>(p);
+    for (int sp = 1; sp < a.nsplit; ++sp) {
+      const float4 x = *reinterpret_cast<const float4*>(p + (int64_t)sp * 2 * stride);
+      s.x += x.x;
+      s.y += x.y;
+      s.z += x.z;
+      s.w += x.w;
+    }
+    T* out = role == 0 ? static_cast<T*>(a.dv) + b * a.dvs[0] + t * a.dvs[1] + hkv * a.dvs[2]
+                       : static_cast<T*>(a.dk) + b * a.dks[0] + t * a.dks[1] + hkv * a.dks[2];
+    *reinterpret_cast<uint2*>(out + d4) = pack4<T>(s.x, s.y, s.z, s.w);
   }
 }
 
@@ -568,7 +620,7 @@ template <typename T, int D>
 int launch(const BwdArgs& a, bool causal, hipStream_t s) {
   const int gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
   const int64_t dq_blocks = (int64_t)((a.S + 32 * (4 / gp) - 1) / (32 * (4 / gp))) * a.B * a.Hq / gp;
-  const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv;
+  const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv * a.nsplit;
   if (causal) {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, true>), dim3(kv_blocks), dim3(NT2), 0, s, a);
@@ -576,20 +628,54 @@ int launch(const BwdArgs& a, bool causal, hipStream_t s) {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   }
+  if (a.nsplit > 1) {
+    const int64_t n = a.rows * a.Hkv * (D / 4);
+    hipLaunchKernelGGL((dkdv_sum_kernel<T, D>), dim3((n + 255) / 256), dim3(256), 0, s, a);
+  }
   return launched("pk_attn_bwd");
 }
 
+// Number of q-head splits of the dk/dv kernel: the smallest divisor of the
+// group size that gives at least two blocks per CU, else the group size (one
+// q head per block). 1 keeps the direct path with no partials.
+int dkdv_splits(int64_t seqs, int64_t seq, int64_t kv_heads, int64_t group) {
+  const int64_t blocks = (seq + BK - 1) / BK * seqs * kv_heads;
+  const int64_t want = 2 * (int64_t)cu_count();
+  for (int64_t d = 1; d <= group; ++d)
+    if (group % d == 0 && (blocks * d >= want || d == group)) return (int)d;
+  return 1;
+}
+
+constexpr int64_t kAlign = 256;
+inline int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace bytes: D and lse2 (2 * lse_n floats), then the dk/dv partials when
+// the kernel splits the q heads.
+int64_t workspace_bytes(int64_t lse_n, int64_t rows, int64_t kv_heads, int64_t head_dim, int nsplit) {
+  const int64_t parts = nsplit > 1 ? (int64_t)nsplit * 2 * rows * kv_heads * head_dim * (int64_t)sizeof(float) : 0;
+  return round_up(2 * lse_n * (int64_t)sizeof(float)) + parts;
+}
+
 // strides[24] = q, k, v, o, dout, dq, dk, dv (batch, token, head)
-int bwd_launch(const char* who, BwdArgs a, const int64_t* strides, int64_t batch, int64_t seq, int64_t q_heads,
-               int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
+int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_bytes_given, const int64_t* strides,
+               int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
+               int causal, int dtype, void* stream) {
   if (batch < 0 || seq < 0 || q_heads < 0 || kv_heads < 0 || head_dim < 0)
     return fail(PK_ERR_INVALID, "%s: negative size", who);
   if (batch == 0 || seq == 0 || q_heads == 0) return PK_OK;
-  if (!a.q || !a.k || !a.v || !a.o || !a.dout || !a.lse || !a.dsum || !a.dq || !a.dk || !a.dv || !strides)
+  if (!a.q || !a.k || !a.v || !a.o || !a.dout || !a.lse || !workspace || !a.dq || !a.dk || !a.dv || !strides)
     return fail(PK_ERR_INVALID, "%s: null pointer", who);
   if (kv_heads == 0 || q_heads % kv_heads != 0)
     return fail(PK_ERR_INVALID, "%s: q_heads=%lld is not a multiple of kv_heads=%lld", who, (long long)q_heads,
                 (long long)kv_heads);
+  a.nsplit = dkdv_splits(batch, seq, kv_heads, q_heads / kv_heads);
+  const int64_t need = workspace_bytes(a.lse_n, a.rows, kv_heads, head_dim, a.nsplit);
+  if (workspace_bytes_given < need)
+    return fail(PK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", who, (long long)workspace_bytes_given,
+                (long long)need);
+  if (!aligned16(workspace)) return fail(PK_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+  a.dsum = static_cast<float*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(2 * a.lse_n * (int64_t)sizeof(float)));
   if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
   if (head_dim != 64 && head_dim != 128)
     return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (64 or 128 only)", who, (long long)head_dim);
@@ -629,10 +715,27 @@ int bwd_launch(const char* who, BwdArgs a, const int64_t* strides, int64_t batch
 
 extern "C" {
 
+int64_t pk_attn_bwd_workspace(int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim) {
+  using namespace pk;
+  if (batch < 0 || seq < 0 || q_heads < 0 || kv_heads <= 0 || head_dim < 0 || q_heads % kv_heads != 0) return -1;
+  const int nsplit = dkdv_splits(batch, seq, kv_heads, q_heads / kv_heads);
+  return workspace_bytes(batch * q_heads * seq, batch * seq, kv_heads, head_dim, nsplit);
+}
+
+int64_t pk_attn_varlen_bwd_workspace(int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                                     int64_t kv_heads, int64_t head_dim) {
+  using namespace pk;
+  if (num_seqs < 0 || total < 0 || max_seqlen < 0 || q_heads < 0 || kv_heads <= 0 || head_dim < 0 ||
+      q_heads % kv_heads != 0)
+    return -1;
+  const int nsplit = dkdv_splits(num_seqs, max_seqlen, kv_heads, q_heads / kv_heads);
+  return workspace_bytes(q_heads * total, total, kv_heads, head_dim, nsplit);
+}
+
 int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
-                float* dsum, void* dq, void* dk, void* dv, const int64_t* strides, int64_t batch, int64_t seq,
-                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype,
-                void* stream) {
+                void* workspace, int64_t workspace_bytes, void* dq, void* dk, void* dv, const int64_t* strides,
+                int64_t batch, int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float softmax_scale,
+                int causal, int dtype, void* stream) {
   using namespace pk;
   BwdArgs a{};
   a.q = q;
@@ -641,7 +744,6 @@ int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   a.o = o;
   a.dout = dout;
   a.lse = lse;
-  a.dsum = dsum;
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;
@@ -649,14 +751,15 @@ int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
   a.lse_bs = q_heads * seq;  // [batch, q_heads, seq]
   a.lse_hs = seq;
   a.lse_n = batch * q_heads * seq;
-  return bwd_launch("pk_attn_bwd", a, strides, batch, seq, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
-                    stream);
+  a.rows = batch * seq;
+  return bwd_launch("pk_attn_bwd", a, workspace, workspace_bytes, strides, batch, seq, q_heads, kv_heads, head_dim,
+                    softmax_scale, causal, dtype, stream);
 }
 
 int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
-                       float* dsum, void* dq, void* dk, void* dv, const int* cu_seqlens, const int64_t* strides,
-                       int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads, int64_t kv_heads,
-                       int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
+                       void* workspace, int64_t workspace_bytes, void* dq, void* dk, void* dv, const int* cu_seqlens,
+                       const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
+                       int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
   using namespace pk;
   const char* who = "pk_attn_varlen_bwd";
   if (num_seqs < 0 || total < 0 || max_seqlen < 0) return fail(PK_ERR_INVALID, "%s: negative size", who);
@@ -678,7 +781,6 @@ int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* 
   a.o = o;
   a.dout = dout;
   a.lse = lse;
-  a.dsum = dsum;
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;
@@ -687,8 +789,9 @@ int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* 
   a.lse_bs = 0;  // [q_heads, total]
   a.lse_hs = total;
   a.lse_n = q_heads * total;
-  return bwd_launch(who, a, dense, num_seqs, max_seqlen, q_heads, kv_heads, head_dim, softmax_scale, causal, dtype,
-                    stream);
+  a.rows = total;
+  return bwd_launch(who, a, workspace, workspace_bytes, dense, num_seqs, max_seqlen, q_heads, kv_heads, head_dim,
+                    softmax_scale, causal, dtype, stream);
 }
 
 }  // extern "C"

@@ -549,13 +549,17 @@ class _Attention(torch.autograd.Function):
         q_, k_, v_, do_ = (_aligned_rows(t) for t in (q, k, v, do.to(q.dtype)))
         dq, dk, dv = torch.empty(q.shape, dtype=q.dtype, device=q.device), torch.empty_like(k_), torch.empty_like(v_)
         dk, dv = dk.contiguous(), dv.contiguous()
-        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=lse.device)  # D, lse2
         lib = _lib.load()
+        # D, lse2 and (for grids too small to fill the device) dk/dv partials of q-head splits
+        nbytes = lib.pk_attn_bwd_workspace(batch, seq, q_heads, k.shape[2], head_dim)
+        if nbytes < 0:
+            raise _lib.KernelError(f"pk_attn_bwd_workspace: invalid shape {tuple(q.shape)} / {tuple(k.shape)}")
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         strides = (_lib._i64 * 24)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:3]))
         _lib.check(
             lib.pk_attn_bwd(
                 q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
-                dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), strides, batch, seq, q_heads,
+                ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), strides, batch, seq, q_heads,
                 k.shape[2], head_dim, _scale(head_dim, ctx.softmax_scale), int(ctx.causal), _lib.dtype_code(q.dtype),
                 _lib.stream_handle(q.device),
             ),
@@ -649,13 +653,16 @@ class _AttentionVarlen(torch.autograd.Function):
         dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
         dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-        dsum = torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=lse.device)  # D, lse2
         lib = _lib.load()
+        nbytes = lib.pk_attn_varlen_bwd_workspace(num_seqs, total, longest, q_heads, k.shape[1], head_dim)
+        if nbytes < 0:
+            raise _lib.KernelError(f"pk_attn_varlen_bwd_workspace: invalid shape {tuple(q.shape)} / {tuple(k.shape)}")
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         strides = (_lib._i64 * 16)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:2]))
         _lib.check(
             lib.pk_attn_varlen_bwd(
                 q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
-                dsum.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), strides, num_seqs,
+                ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), strides, num_seqs,
                 total, longest, q_heads, k.shape[1], head_dim, _scale(head_dim, softmax_scale), int(causal),
                 _lib.dtype_code(q.dtype), _lib.stream_handle(q.device),
             ),

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import reference as O
-from popcorn_amd import impls
+from popcorn_amd import _lib, impls
 from popcorn_amd.compat import references as R
 from tests._parity import gauge_ok, seeded
 
@@ -146,3 +146,42 @@ def test_attn_bwd_long_causal_against_float64_on_device():
         err = (got.double() - want).abs().max().item()
         scale = max(1.0, want.abs().max().item())
         assert err <= 2e-2 * scale, f"{name}: {err:.3e} vs {scale:.2f}"
+
+
+def _lse_bytes(b, s, hq):
+    return -(-2 * b * hq * s * 4 // 256) * 256  # D and lse2, rounded up to 256 bytes
+
+
+def test_attn_bwd_split_and_direct_paths_agree():
+    """B=8, S=1024, 32 q heads over 8 kv heads fills the device (512 dk/dv blocks), so dk/dv are written
+    directly; sequence 0 alone (64 blocks) takes the q-head split, whose four fp32 partials are added in
+    order. Both round once to bf16, so they agree to within one bf16 unit."""
+    b, s, hq, hkv, d = 8, 1024, 32, 8, 128
+    lib = _lib.load()
+    assert lib.pk_attn_bwd_workspace(b, s, hq, hkv, d) == _lse_bytes(b, s, hq)  # no partials: direct path
+    assert lib.pk_attn_bwd_workspace(1, s, hq, hkv, d) > _lse_bytes(1, s, hq)  # partials: split path
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(b, s, hkv, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    full = [t.clone().requires_grad_() for t in (q, k, v)]
+    g_full = torch.autograd.grad(impls.attn(*full, True), full, do)
+    one = [t[:1].clone().requires_grad_() for t in (q, k, v)]
+    g_one = torch.autograd.grad(impls.attn(*one, True), one, do[:1])
+    for name, a, c in zip(("dq", "dk", "dv"), g_full, g_one):
+        torch.testing.assert_close(a[:1].float(), c.float(), rtol=2**-7, atol=1e-5, msg=name)
+
+
+def test_attn_bwd_rejects_a_short_workspace():
+    b, s, hq, hkv, d = 1, 256, 8, 2, 128
+    lib = _lib.load()
+    need = lib.pk_attn_bwd_workspace(b, s, hq, hkv, d)
+    assert need > _lse_bytes(b, s, hq)
+    q, k, v, do = (seeded((b, s, h, d), i, torch.bfloat16).to(DEV) for i, h in enumerate((hq, hkv, hkv, hq)))
+    o, lse = impls.attn_with_lse(q, k, v, True)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    st = (_lib._i64 * 24)(*(x for t in (q, k, v, o, do, dq, dk, dv) for x in t.stride()[:3]))
+    rc = lib.pk_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+                         ws.data_ptr(), need - 1, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), st, b, s, hq, hkv, d,
+                         d**-0.5, 1, _lib.BF16, _lib.stream_handle(q.device))
+    assert rc != 0 and b"workspace" in lib.pk_last_error()
