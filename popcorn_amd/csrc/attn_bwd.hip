@@ -22,7 +22,11 @@
 //               the roles halves each wave's registers (one fragment set, one
 //               accumulator), which is what lets two waves share each SIMD.
 //               Query tiles (with their lse2 and D rows) arrive two steps ahead
-//               through four LDS stages.
+//               through four LDS stages. A block walks its q heads' tiles one
+//               after another, so when the grid is too small to fill the
+//               device the q heads of each group are split over several blocks
+//               that leave fp32 partials, and a third kernel adds them in
+//               split order (still deterministic).
 //
 // Both kernels stage tiles with buffer loads that write LDS directly (16
 // bytes per lane at the wave's LDS base + 16 * lane): each lane fetches the
