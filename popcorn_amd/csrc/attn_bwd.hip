@@ -137,8 +137,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int n_quads = G / GP;
   const int per_tile = a.B * a.Hkv * n_quads;
   const int w = blockIdx.x;
-  const int m_tile = m_tiles - 1 - w / per_tile;
-  const int rest = w % per_tile;
+  int m_tile, rest;
+  if (per_tile % 8 == 0) {  // group-major per XCD, as in the forward
+    const int k = w >> 3;
+    m_tile = m_tiles - 1 - k % m_tiles;
+    rest = (w & 7) + 8 * (k / m_tiles);
+  } else {
+    m_tile = m_tiles - 1 - w / per_tile;
+    rest = w % per_tile;
+  }
   const int b = rest / (a.Hkv * n_quads);
   const int hkv = (rest / n_quads) % a.Hkv;
   const int hq = hkv * G + (rest % n_quads) * GP + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % GP;
@@ -332,10 +339,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 
   const int w = blockIdx.x;
   const int per_tile = a.B * a.Hkv * a.nsplit;
-  const int kv_tile = w / per_tile;  // first key tiles (the most causal work) first
-  const int b = (w % per_tile) / (a.Hkv * a.nsplit);
-  const int hkv = (w / a.nsplit) % a.Hkv;
-  const int split = w % a.nsplit;
+  // first key tiles (the most causal work) first. (Group-major order per XCD,
+  // as the forward and dq kernels use, measured 26 % more HBM fetch here: a
+  // block streams its group's whole Q/dO from its own key tile on, and the
+  // 32 resident blocks of one group start at 32 different places.)
+  const int kv_tile = w / per_tile;
+  const int gi = w % per_tile;
+  const int b = gi / (a.Hkv * a.nsplit);
+  const int hkv = (gi / a.nsplit) % a.Hkv;
+  const int split = gi % a.nsplit;
   const int heads = a.group / a.nsplit;  // q heads this block walks, from split * heads on
   int start, S;
   seq_bounds(a, b, start, S);
