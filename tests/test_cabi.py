@@ -48,6 +48,28 @@ def test_version_and_status_codes(lib):
         assert re.search(rf"#define {name} {value}\b", text), name
 
 
+def test_attention_backward_workspace_queries(lib):
+    """Host logic only: two fp32 row vectors (D and log2-scaled lse) per (row, q head), padded to 256 bytes,
+    plus fp32 dK and dV partials per q-head split when a grid of 128-key blocks cannot fill a 256-CU device
+    twice over (this container has no device, so the library assumes MI355X's 256 CUs)."""
+    mib = 1 << 20
+    # B=8, S=1024, 32/8 heads: 8 key blocks x 8 x 8 = 512 blocks = two per CU, so no split
+    assert lib.pk_attn_bwd_workspace(8, 1024, 32, 8, 128) == 2 * 8 * 32 * 1024 * 4 == 2 * mib
+    # B=1: 64 blocks; no divisor of the group of 4 reaches 512, so one q head per block (4 splits)
+    assert lib.pk_attn_bwd_workspace(1, 1024, 32, 8, 128) == 2 * 32 * 1024 * 4 + 4 * 2 * 1024 * 8 * 128 * 4
+    # B=4, S=1024: 256 blocks, two splits give 512
+    assert lib.pk_attn_bwd_workspace(4, 1024, 32, 8, 64) == 2 * 4 * 32 * 1024 * 4 + 2 * 2 * 4 * 1024 * 8 * 64 * 4
+    assert lib.pk_attn_bwd_workspace(1, 3, 1, 1, 64) == 256  # 6 floats, padded; a group of one never splits
+    assert lib.pk_attn_bwd_workspace(0, 1024, 32, 8, 128) == 0
+    for bad in ((-1, 8, 4, 4, 64), (1, 8, 6, 4, 64), (1, 8, 4, 0, 64), (1, -8, 4, 4, 64)):
+        assert lib.pk_attn_bwd_workspace(*bad) == -1, bad
+    # packed sequences: rows = total tokens, blocks counted at the longest sequence
+    assert lib.pk_attn_varlen_bwd_workspace(64, 64 * 1024, 1024, 32, 8, 128) == 2 * 32 * 64 * 1024 * 4
+    assert lib.pk_attn_varlen_bwd_workspace(2, 1500, 1024, 8, 2, 128) == (
+        (2 * 8 * 1500 * 4 + 255) // 256 * 256 + 4 * 2 * 1500 * 2 * 128 * 4)
+    assert lib.pk_attn_varlen_bwd_workspace(2, 1500, 1024, 8, 3, 128) == -1
+
+
 def test_invalid_arguments_are_rejected_before_any_launch(lib):
     assert lib.pk_swiglu_fwd(None, None, None, -1, _lib.BF16, None) == _lib.ERR_INVALID
     assert "negative size" in lib.pk_last_error().decode()
