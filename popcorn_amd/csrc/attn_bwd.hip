@@ -16,7 +16,7 @@
 //               LDS. The slice's role-0 wave holds K and computes S = Q K^T,
 //               whose result layout puts one key per lane column, so
 //               P = exp2(s*c - lse2) goes straight into dV^T += dO^T P as the
-//               B operand; it also leaves P (fp32) in LDS. The role-1 wave
+//               B operand; it also leaves P (as fp16) in LDS. The role-1 wave
 //               holds V, computes dP = dO V^T one step later, reads that P,
 //               forms dS = P (dP - D) and accumulates dK^T += Q^T dS. Splitting
 //               the roles halves each wave's registers (one fragment set, one
@@ -334,8 +334,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) T QG[NS][2 * TILE];
   __shared__ __attribute__((aligned(16))) float RV[NS][2][64];
   __shared__ __attribute__((aligned(16))) float spill[64];
-  // P of each key slice, fp32, double-buffered: [buffer][slice][16 values x 64 lanes]
-  __shared__ __attribute__((aligned(16))) float Pb[2][4][16 * 64];
+  // P of each key slice as fp16 (P <= 1; 11 significant bits, more than the
+  // rounded dS it feeds), double-buffered: [buffer][slice][16 values x 64 lanes]
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(16))) _Float16 Pb[2][4][16 * 64];
 
   const int w = blockIdx.x;
   const int per_tile = a.B * a.Hkv * a.nsplit;
@@ -467,8 +469,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       out[4 * j + 3] = x.w;
     }
   };
-  // P buffer layout: value r of lane l at (r / 4) * 256 + 4 * l + r % 4 (16-byte lane stride)
-  float* pmine = nullptr;
+  // P buffer layout: value r of lane l at (r / 8) * 512 + 8 * l + r % 8 (16-byte lane stride)
 
   // Step t: role 0 takes tile t (P into Pb[t & 1]), role 1 tile t - 1 (P from
   // Pb[(t - 1) & 1]). Tile t + NS - 2 is issued into the stage of tile t - 2,
@@ -477,7 +478,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   for (int j = 0; j < NS - 2; ++j) issue(j);
   loads_landed_but<(NS - 3) * PER_ISSUE>();
   __syncthreads();
-  (void)pmine;
   // One step's 16 products: 8 of the score block (A from the tile at `pbase`,
   // B = the lane's key row) then 8 of the accumulation (A^T from transposing
   // reads of the tile at `abase`, B from `mid`, which turns the score block
@@ -528,7 +528,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
         rows16(RV[st][0], l2);
         // tiles wholly before this slice's keys (causal) are masked to zero, not skipped
         const bool need_mask = (CAUSAL && q0 < kw0 + 32) || !key_ok || q0 + BQ > S;
-        float* pw = Pb[t & 1][slice];
+        _Float16* pw = Pb[t & 1][slice];
         run16(qs, qs + TILE, [&](const f32x16& s, Frag (&pf)[2]) {
           float p[16];
 #pragma unroll
@@ -540,8 +540,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
             }
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<float4*>(pw + 256 * j + 4 * lane) = make_float4(p[4 * j], p[4 * j + 1], p[4 * j + 2], p[4 * j + 3]);
+          for (int j = 0; j < 2; ++j) {
+            h8 hv;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hv[i] = (_Float16)p[8 * j + i];
+            *reinterpret_cast<h8*>(pw + 512 * j + 8 * lane) = hv;
+          }
 #pragma unroll
           for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -554,14 +558,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       const T* qs = QG[st];
       float dd[16], p[16];
       rows16(RV[st][1], dd);
-      const float* pr = Pb[u & 1][slice];
+      const _Float16* pr = Pb[u & 1][slice];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 x = *reinterpret_cast<const float4*>(pr + 256 * j + 4 * lane);
-        p[4 * j] = x.x;
-        p[4 * j + 1] = x.y;
-        p[4 * j + 2] = x.z;
-        p[4 * j + 3] = x.w;
+      for (int j = 0; j < 2; ++j) {
+        const h8 x = *reinterpret_cast<const h8*>(pr + 512 * j + 8 * lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[8 * j + i] = (float)x[i];
       }
       run16(qs + TILE, qs, [&](const f32x16& dp, Frag (&dsf)[2]) {
 #pragma unroll
