@@ -61,7 +61,7 @@ constexpr int BN = 32;   // dq kernel: keys per tile
 constexpr int BK = 128;  // dkdv kernel: keys per block
 constexpr int BQ = 32;   // dkdv kernel: query rows per tile
 constexpr int kRingDq = 3;    // dq kernel: fragment reads in flight ahead of their product
-constexpr int kRingDkdv = 4;  // dkdv kernel: the same
+constexpr int kRingDkdv = 5;  // dkdv kernel: the same
 
 struct BwdArgs {
   const void *q, *k, *v, *o, *dout;
