@@ -86,6 +86,24 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
                    void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream);
 
 /*
+ * pk_rmsnorm_bwd without a workspace argument and without any allocation:
+ * the dw / dbias partial rows and the column-sum stage live in a fixed
+ * file-scope device array of 96 MiB (100,663,296 bytes), which every GPU the
+ * library runs on holds until the process ends. The kernels, grid and
+ * summation order are pk_rmsnorm_bwd's, so the results are identical bit for
+ * bit. A shape whose partial rows and stage do not fit the array (their size
+ * is at most pk_rmsnorm_bwd_workspace) is refused with PK_ERR_UNSUPPORTED
+ * before any launch: measured on MI355X, 65,536 rows of 8192 columns fit
+ * (69 MB), and with dbias rows of 4096 columns. Calls that overlap on one GPU
+ * (other streams or threads) share the array and race; serialise them.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).
+ */
+int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw,
+                           void* dbias, int64_t rows, int64_t cols, int dtype, void* stream);
+
+/*
  * Residual add fused with RMSNorm, over `rows` contiguous rows of `cols`:
  *   s = round(x + residual); r = 1/sqrt(mean(s^2) + eps);
  *   y = round(round(s*r) * round(w + offset)).

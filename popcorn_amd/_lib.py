@@ -34,6 +34,7 @@ SIGNATURES = {
     "pk_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _f32, _int, _p]),
     "pk_rmsnorm_bwd_workspace": (_i64, [_i64, _i64, _int]),
     "pk_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _p]),
+    "pk_rmsnorm_bwd_noalloc": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _int, _p]),
     "pk_add_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _int, _p]),
     "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _p]),
     "pk_rotary": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),

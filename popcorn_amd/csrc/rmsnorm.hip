@@ -23,6 +23,8 @@
 // sums the partials in a fixed order, so dw is deterministic.
 #include <math.h>
 
+#include <mutex>
+
 #include "api.h"
 #include "colsum.h"
 #include "common.h"
@@ -711,6 +713,47 @@ int check_shape(const char* who, int64_t rows, int64_t cols, int dtype) {
 }  // namespace
 }  // namespace pk
 
+// ---------------------------------------------------------------------------
+// Fixed scratch for pk_rmsnorm_bwd_noalloc: the dw / dbias partial rows and
+// the column-sum stage of one backward call. Every GPU the library runs on
+// holds its own copy from module load until the process ends. Each block
+// writes its whole partial row and the first column-sum stage writes every
+// stage row it covers, so nothing needs clearing between calls; two calls that
+// overlap on one GPU (on different streams, or from different threads) share
+// the array and race.
+static constexpr int64_t kScratchBytes = (int64_t)96 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace pk {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_addr[kMaxDevices];  // device address of `scratch` per device, once looked up
+
+// Device address of the current device's scratch array. The array's host-side
+// name is only a stand-in for the symbol: its device address is looked up
+// once per device with that device current and kept.
+int scratch_address(const char* who, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(PK_ERR_HIP, "%s: no current HIP device", who);
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* addr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || addr == nullptr)
+      return fail(PK_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", who, dev,
+                  hipGetErrorString(err));
+    g_scratch_addr[dev] = addr;
+  }
+  *out = g_scratch_addr[dev];
+  return PK_OK;
+}
+
+}  // namespace
+}  // namespace pk
+
 extern "C" {
 
 int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, float* rstd, int64_t rows, int64_t cols,
@@ -744,6 +787,27 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
   BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
   if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, mode, a)) return st;
+  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, who) : bwd_dispatch<kPlain>(a, dtype, who);
+}
+
+int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw,
+                           void* dbias, int64_t rows, int64_t cols, int dtype, void* stream) {
+  using namespace pk;
+  const char* who = "pk_rmsnorm_bwd_noalloc";
+  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (cols == 0) return fail(PK_ERR_INVALID, "%s: zero-width rows", who);
+  if (!x || !w || !rstd || !dy || !dx || !dw) return fail(PK_ERR_INVALID, "%s: null pointer", who);
+  if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "%s: zero rows (dw is all zeros; fill it host-side)", who);
+  const int mode = dbias != nullptr ? kBias : kPlain;
+  const int64_t need = workspace_layout(rows, cols, dtype, mode).total;
+  if (need > kScratchBytes)
+    return fail(PK_ERR_UNSUPPORTED, "%s: shape (%lld, %lld) needs %lld bytes of scratch, the fixed array holds %lld",
+                who, (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
+  void* base = nullptr;
+  if (int st = scratch_address(who, &base)) return st;
+  BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,
+            static_cast<hipStream_t>(stream)};
+  if (int st = carve(who, base, kScratchBytes, rows, cols, dtype, mode, a)) return st;
   return mode == kBias ? bwd_dispatch<kBias>(a, dtype, who) : bwd_dispatch<kPlain>(a, dtype, who);
 }
 
