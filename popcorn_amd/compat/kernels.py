@@ -11,7 +11,7 @@ import torch
 from torch import Tensor
 
 from popcorn_amd.compat import references
-from popcorn_amd.compat.dispatcher import register_kernel
+from popcorn_amd.compat.ops import register_kernel
 from popcorn_amd.compat.shapes import Float, Int32
 
 

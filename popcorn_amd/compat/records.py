@@ -1,11 +1,12 @@
-"""Call configurations and report rows (schema 3).
+"""Case configurations and report rows (schema 3).
 
-A call is summarised as a canonical config -- dims, batch extent, dtype,
-scalar args and which optional tensors are present -- and a stable 12-hex
-`config_id` (core/config.py:38-114). One validation / benchmark outcome is a
+A case is summarised as a canonical config -- dims, batch extent, dtype,
+scalar args and which optional tensors are present -- with a stable 12-hex
+`config_id` (core/config.py:38-64). One validation / benchmark outcome is a
 `Record` whose dictionary form is Popcorn's report-row schema 3
-(bench/model.py:105-163). The id scheme and the row keys are kept identical to
-Popcorn's so rows written here and rows Popcorn writes name the same cases.
+(bench/model.py:105-163). The config layout, the id's hash payload and the row
+keys are a format shared with Popcorn: rows written here and rows Popcorn
+writes name the same cases and merge in either direction.
 """
 
 from __future__ import annotations
@@ -16,14 +17,9 @@ import math
 import platform
 from collections.abc import Iterable, Mapping
 from dataclasses import asdict, dataclass, field
-from typing import TYPE_CHECKING, Any
+from typing import Any
 
 import torch
-
-from popcorn_amd.compat.shapes import batch_shape
-
-if TYPE_CHECKING:
-    from popcorn_amd.compat.dispatcher import Dispatcher
 
 SCHEMA = 3
 
@@ -84,43 +80,6 @@ def device_name(device: torch.device | str | int | None = None) -> str:
 
 
 @dataclass(frozen=True)
-class Call:
-    """One dispatchable call: its config, whether it needs gradients, its device."""
-
-    config: dict
-    grad: bool
-    device: torch.device
-    device_name: str
-
-
-def call_config(op: Dispatcher, values: Mapping[str, Any], arguments: Mapping[str, Any]) -> Call | None:
-    """The call's canonical config, or None when it has no single one (mixed float
-    dtypes or devices, inconsistent batch extents)."""
-    dims = {name: values[name] for name in op._dims if name in values}
-    if set(dims) != set(op._dims):
-        return None
-    if any(... in spec.tokens for spec in op.specs):
-        batch = batch_shape(op.specs, arguments)
-        if batch is None:
-            return None
-    else:
-        batch = ()
-    dtype = dtype_name(values.get("dtype"))
-    if dtype is None:
-        if any("float" in d for spec in op.specs for d in spec.dtypes):
-            return None
-        dtype = "float32"
-    devices = {v.device for v in arguments.values() if isinstance(v, torch.Tensor)}
-    if len(devices) > 1:
-        return None
-    device = next(iter(devices), torch.device("cpu"))
-    present = (spec.param for spec in op.specs if spec.optional and arguments[spec.param] is not None)
-    config = make_config(dims, batch, dtype, {name: arguments[name] for name in op.arg_pools}, present)
-    grad = torch.is_grad_enabled() and any(isinstance(v, torch.Tensor) and v.requires_grad for v in arguments.values())
-    return Call(config, grad, device, device_name(device))
-
-
-@dataclass(frozen=True)
 class Case:
     """One grid point: dims, batch extent, dtype, scalar args, present optionals."""
 
@@ -167,13 +126,19 @@ class Gauge:
         peak = truth.detach().abs().max().item() if truth.numel() else 1.0
         self.scale = max(self.scale, peak)
 
+    def allowance(self, floor: float) -> float:
+        """The largest error that passes: twice the reference's own error, or the dtype floor at the truth's scale."""
+        return max(2 * self.budget, floor * self.scale)
+
     def verdict(self, floor: float) -> str | None:
-        """None when err <= max(2 * budget, floor * scale) (bench/model.py:66-71), else the reason."""
-        if not math.isfinite(self.err):
-            return "err is non-finite"
-        if self.err <= max(2 * self.budget, floor * self.scale):
-            return None
-        return f"err {self.err:.3e} > max(2*{self.budget:.3e}, {floor:.0e}*{self.scale:.1f})"
+        """None when the worst error is within `allowance(floor)` (bench/model.py:66-71), else why not."""
+        if math.isnan(self.err) or math.isinf(self.err):
+            return "error is not finite"
+        limit = self.allowance(floor)
+        if self.err > limit:
+            return (f"error {self.err:.3e} above {limit:.3e} (2 x budget {self.budget:.3e}, "
+                    f"floor {floor:.0e} x scale {self.scale:.1f})")
+        return None
 
 
 @dataclass
@@ -232,22 +197,30 @@ class Record:
 
     @classmethod
     def from_dict(cls, row: Mapping[str, Any]) -> Record:
-        if row.get("schema") != SCHEMA:
-            raise ValueError(f"unsupported report schema {row.get('schema')!r}; expected {SCHEMA}")
+        """Rebuild a record from its row; rows of any other schema are refused."""
+        schema = row.get("schema")
+        if schema != SCHEMA:
+            raise ValueError(f"report row has schema {schema!r}; this reader takes schema {SCHEMA} only")
+        gauges = {side: {name: Gauge(**fields) for name, fields in (row.get(side) or {}).items()}
+                  for side in ("fwd", "bwd")}
+        bench = dict(row.get("bench") or {})
         result = Result(
             status=row["status"],
-            reason=row.get("reason", ""),
-            grad=row["grad"],
-            fwd={k: Gauge(**v) for k, v in (row.get("fwd") or {}).items()},
-            bwd={k: Gauge(**v) for k, v in (row.get("bwd") or {}).items()},
-            bench=dict(row.get("bench") or {}),
-            benchmarked=row.get("benchmarked", bool(row.get("bench"))),
-            bench_error=row.get("bench_error", "") or "",
-            reps=row.get("reps", 0) or 0,
+            reason=row.get("reason") or "",
+            grad=bool(row["grad"]),
+            fwd=gauges["fwd"],
+            bwd=gauges["bwd"],
+            bench=bench,
+            # rows written before the flag existed count as benchmarked when they carry timings
+            benchmarked=bool(row["benchmarked"]) if row.get("benchmarked") is not None else bool(bench),
+            bench_error=row.get("bench_error") or "",
+            reps=int(row.get("reps") or 0),
         )
-        env = Environment(row["device"], row["torch"], row.get("backend_version"), row["ts"], row.get("ref_hash"),
-                          row.get("impl_hash"))
-        return cls(row["op"], row["impl"], row.get("case", ""), row["case_id"], row["config"], env, result)
+        environment = Environment(
+            device=row["device"], torch=row["torch"], backend_version=row.get("backend_version"), ts=row["ts"],
+            ref_hash=row.get("ref_hash"), impl_hash=row.get("impl_hash"),
+        )
+        return cls(row["op"], row["impl"], row.get("case") or "", row["case_id"], row["config"], environment, result)
 
     @property
     def key(self) -> tuple[Any, ...]:

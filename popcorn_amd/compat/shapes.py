@@ -12,7 +12,8 @@ and the three operations dispatch needs from it:
     whether they are optional;
   * `extract(specs, arguments)`: bind every dim name to one size across all
     tensors (a mismatch is a DispatchError naming the dim);
-  * `matches(value, annotation)` / `narrows(sub, sup)`: the gate checks.
+  * `satisfies(value, annotation)` / `narrower(sub, sup)`: the gate checks,
+    over annotations flattened into their alternatives.
 
 Dim tokens are names, integer literals or `...` (the batch extent). Derived
 dims (`seq+1`) are not needed by the four transformer-block ops and are not
@@ -187,46 +188,86 @@ def batch_shape(specs: tuple[TensorSpec, ...], arguments: Mapping[str, Any]) -> 
     return next(iter(seen), ())
 
 
-def _norm(annotation: Any) -> Any:
-    return type(None) if annotation is None else annotation
+@dataclass(frozen=True)
+class _Exactly:
+    """One value of a `Literal[...]` annotation."""
+
+    value: Any
 
 
-def matches(value: Any, annotation: Any) -> bool:
-    """Does `value` satisfy `annotation` (Literal, union, None, class, tensor type)?"""
-    annotation = _norm(annotation)
+def _alternatives(annotation: Any) -> tuple[Any, ...]:
+    """An annotation flattened into the alternatives a value may satisfy.
+
+    Unions (and `X | None`) contribute each member, `Literal[a, b]` one
+    `_Exactly` per value, `None` the class of None, and an absent annotation or
+    `Any` the single alternative `Any`. Anything else stands for itself.
+    """
+    if annotation is None:
+        return (type(None),)
     if annotation is inspect.Parameter.empty or annotation is typing.Any:
-        return True
+        return (typing.Any,)
     origin = typing.get_origin(annotation)
-    if origin is typing.Literal:
-        return any(value is a or (type(value) is type(a) and value == a) for a in typing.get_args(annotation))
     if origin in _UNIONS:
-        return any(matches(value, member) for member in typing.get_args(annotation))
-    if isinstance(annotation, TensorType):
-        return isinstance(value, torch.Tensor) and str(value.dtype).removeprefix("torch.") in annotation.dtypes
-    if isinstance(annotation, type):
-        return isinstance(value, annotation)
-    return True
+        return tuple(alt for member in typing.get_args(annotation) for alt in _alternatives(member))
+    if origin is typing.Literal:
+        return tuple(_Exactly(value) for value in typing.get_args(annotation))
+    return (annotation,)
 
 
-def narrows(sub: Any, sup: Any) -> bool:
-    """Is every value admitted by `sub` also admitted by `sup`?"""
-    sub, sup = _norm(sub), _norm(sup)
-    if sup is inspect.Parameter.empty or sup is typing.Any or sub == sup:
+def _admits(alternative: Any, value: Any) -> bool:
+    if alternative is typing.Any:
         return True
-    if typing.get_origin(sub) is typing.Literal:
-        return all(matches(v, sup) for v in typing.get_args(sub))
-    if typing.get_origin(sub) in _UNIONS:
-        return all(narrows(member, sup) for member in typing.get_args(sub))
-    if typing.get_origin(sup) in _UNIONS:
-        return any(narrows(sub, member) for member in typing.get_args(sup))
-    if isinstance(sub, TensorType) and isinstance(sup, TensorType):
-        return sub.dim_str == sup.dim_str and set(sub.dtypes) <= set(sup.dtypes)
-    if isinstance(sub, type) and isinstance(sup, type):
+    if isinstance(alternative, _Exactly):
+        # True == 1 but a bool literal admits only bools: compare the type as well
+        return value is alternative.value or (type(value) is type(alternative.value) and value == alternative.value)
+    if isinstance(alternative, TensorType):
+        return isinstance(value, torch.Tensor) and str(value.dtype).removeprefix("torch.") in alternative.dtypes
+    if isinstance(alternative, type):
         try:
-            return issubclass(sub, sup)
-        except TypeError:
-            return False
-    return False
+            return isinstance(value, alternative)
+        except TypeError:  # parametrised generics: not modelled, so no constraint
+            return True
+    return True  # an annotation this vocabulary does not model constrains nothing
+
+
+def satisfies(value: Any, annotation: Any) -> bool:
+    """Does `value` meet `annotation` (a Literal, union, None, class or tensor type)?"""
+    return any(_admits(alternative, value) for alternative in _alternatives(annotation))
+
+
+def _inside(alternative: Any, wider: tuple[Any, ...]) -> bool:
+    """Is every value `alternative` admits also admitted by one of `wider`?"""
+    if typing.Any in wider:
+        return True
+    if isinstance(alternative, _Exactly):
+        return any(_admits(w, alternative.value) for w in wider)
+    if isinstance(alternative, TensorType):
+        return any(isinstance(w, TensorType) and w.dim_str == alternative.dim_str
+                   and set(alternative.dtypes) <= set(w.dtypes) for w in wider)
+    if isinstance(alternative, type):
+        for w in wider:
+            if isinstance(w, type):
+                try:
+                    if issubclass(alternative, w):
+                        return True
+                except TypeError:
+                    pass
+        return False
+    return alternative in wider
+
+
+def narrower(sub: Any, sup: Any) -> bool:
+    """Does annotation `sub` admit only values that `sup` admits?
+
+    An adapter may narrow a reference annotation (`Literal[True]` for `bool`,
+    `BFloat16[...]` for `Float[...]`); the narrowed form becomes a dispatch
+    gate. Tensor types narrow when their dims agree and their dtypes are a
+    subset.
+    """
+    if sub == sup:
+        return True
+    wider = _alternatives(sup)
+    return all(_inside(alternative, wider) for alternative in _alternatives(sub))
 
 
 def fmt_value(value: Any) -> str:

@@ -8,7 +8,8 @@ import torch
 
 import popcorn_amd
 from popcorn_amd import backend, compat
-from popcorn_amd.compat.sources import installed_version, unavailable_reason
+from popcorn_amd.compat.backends import installed_version, unavailable_reason
+from popcorn_amd.compat.ops import describe
 
 
 def test_distribution_metadata_resolves_at_the_package_version():
@@ -41,6 +42,5 @@ def test_cpu_tensors_are_declined_and_torch_serves():
     backend.register(compat)
     x, w = torch.randn(4, 8), torch.ones(8)
     op = compat.KERNELS["rms_norm"]
-    values = op._values({"x": x, "weight": w, "bias": None, "eps": 1e-6})
-    assert op[backend.BACKEND].rejects(values, {"x": x, "weight": w, "bias": None, "eps": 1e-6})
+    assert op[backend.BACKEND].refusal(describe(op, (x, w), {}))
     torch.testing.assert_close(op(x, w), compat.references.rms_norm(x, w))

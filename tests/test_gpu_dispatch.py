@@ -4,8 +4,11 @@
 native-dtype budget, timings) and writes a schema-3 row to the user cache;
 a plain `op(...)` afterwards must route to the backend exactly when its
 recorded time beats torch's by more than the 3% indifference margin
-(core/policy.py:30, 164-172). Reference-side attention is evaluated through
-fused SDPA kernels or explicit contiguous products (compat.references.attn).
+(core/policy.py:30, 164-172). The first tests do that at small shapes for
+every op; the `test_baseline_*` tests do it at the five BASELINE configs and
+require the backend to be the one chosen. Reference-side attention is
+evaluated through fused SDPA kernels or explicit contiguous products
+(compat.references.attn).
 """
 
 from __future__ import annotations
@@ -46,8 +49,9 @@ def _randn(*shape, dtype=torch.bfloat16, seed=0):
 
 
 def _selected(op):
-    assert op.tuner._selected, "no selection was made"
-    return list(op.tuner._selected.values())[-1].name
+    choice = op.tuner.last_choice()
+    assert choice is not None, "no selection was made"
+    return choice
 
 
 def _check_record_and_route(op, record, call):
@@ -177,3 +181,71 @@ def test_bench_mode_measures_lazily(monkeypatch):
     assert [(r["impl"], r["status"], r["benchmarked"]) for r in rows] == [(NAME, "pass", True)]
     op(a, b)  # already measured: no new row
     assert len((store.user_reports() / "swiglu.jsonl").read_text().splitlines()) == 1
+
+
+# --------------------------------------------------------------------------- the five BASELINE configs
+
+
+def _auto_selected(op, record, call):
+    """The recorded row passes and beats torch by more than the indifference margin, and a plain call picks it."""
+    r = record.result
+    assert record.impl == NAME and r.status == "pass", (r.status, r.reason)
+    assert r.benchmarked, r.bench_error
+    ours = r.bench["fwd_ms"] + r.bench.get("bwd_ms", 0.0)
+    theirs = r.bench["ref_fwd_ms"] + r.bench.get("ref_bwd_ms", 0.0)
+    print(f"[selected] {op.name} {record.case}: {NAME} {ours:.4f} ms, torch on the GPU {theirs:.4f} ms "
+          f"({theirs / ours:.2f}x)", flush=True)
+    op.tuner.forget()
+    out = call()
+    assert _selected(op) == NAME, f"torch was chosen: {ours:.4f} ms against torch's {theirs:.4f} ms"
+    return out
+
+
+def test_baseline_c1_rms_norm_fp32_forward_is_auto_selected():
+    op = compat.KERNELS["rms_norm"]
+    x = _randn(4096, 4096, dtype=torch.float32)
+    w = 1 + 0.1 * _randn(4096, dtype=torch.float32, seed=1)
+    with torch.no_grad():
+        [record] = op.benchmark(x, w, None, 1e-6, backend=NAME)
+        y = _auto_selected(op, record, lambda: op(x, w, None, 1e-6))
+    assert torch.equal(y, impls.rms_norm(x, w, None, 1e-6))
+
+
+def test_baseline_c2_swiglu_full_size_is_auto_selected():
+    op = compat.KERNELS["swiglu"]
+    a, b = _randn(16384, 14336), _randn(16384, 14336, seed=1)
+    with torch.no_grad():
+        [record] = op.benchmark(a, b, backend=NAME)
+        _auto_selected(op, record, lambda: op(a, b))
+
+
+def test_baseline_c3_rotary_q_and_k_with_bf16_tables_are_auto_selected():
+    """C3's two calls with the harness's all-bf16 tables (its fp32-table form has no single dtype, so no
+    record applies and registration order serves it: test_mixed_dtype_rotary_is_served_in_registration_order)."""
+    op = compat.KERNELS["rotary_embedding"]
+    pos = torch.arange(4096, dtype=torch.float64, device=DEV)[:, None]
+    ang = pos * 500000.0 ** (-torch.arange(64, dtype=torch.float64, device=DEV) / 64)
+    cos, sin = ang.cos().bfloat16(), ang.sin().bfloat16()
+    with torch.no_grad():
+        for heads, seed in ((32, 0), (8, 1)):
+            x = _randn(8, 4096, heads, 128, seed=seed)
+            [record] = op.benchmark(x, cos, sin, backend=NAME)
+            _auto_selected(op, record, lambda: op(x, cos, sin))
+
+
+def test_baseline_c4_rms_norm_bf16_with_grad_is_auto_selected():
+    op = compat.KERNELS["rms_norm"]
+    x = _randn(65536, 8192).requires_grad_()
+    w = (1 + 0.1 * _randn(8192, dtype=torch.float32, seed=1)).bfloat16().requires_grad_()
+    [record] = op.benchmark(x, w, backend=NAME)
+    assert record.result.grad and {"x", "weight"} <= set(record.result.bwd)
+    _auto_selected(op, record, lambda: op(x, w))
+
+
+def test_baseline_c5_causal_gqa_attention_forward_is_auto_selected():
+    op = compat.KERNELS["attn"]
+    q, k, v = _randn(4, 8192, 32, 128), _randn(4, 8192, 8, 128, seed=1), _randn(4, 8192, 8, 128, seed=2)
+    with torch.no_grad():
+        [record] = op.benchmark(q, k, v, True, backend=NAME)
+        assert not record.result.grad
+        _auto_selected(op, record, lambda: op(q, k, v, True))

@@ -95,7 +95,7 @@ def test_publish_upserts_the_user_cache_into_parquet(tmp_path):
     rows = {r.case_id: r for r in store.read_file(reports / "op.parquet")}
     assert set(rows) == {"a", "b"} and rows["a"].result.status == "pass"  # newer conclusive row replaces
     assert not (reports / "other_op.parquet").exists()
-    merged = store.Store(bundled=reports, user=tmp_path / "empty").merged("op")
+    merged = store.Reports(bundled=reports, user=tmp_path / "empty").rows("op")
     assert sorted(r.case_id for r in merged) == ["a", "b"]
 
 
