@@ -13,10 +13,14 @@ calibrate HBM byte counters.
 Rank 0 prints ONE JSON line. `value` is the workload's achieved algorithmic
 throughput (TB/s of HBM bytes for c1-c4, TFLOP/s for c5). `roofline` is the
 dominant kernel's figure, timed with HIP events on the stream it is launched
-on (torch's current stream). `cpu_baseline` times Popcorn's PyTorch reference
+on (torch's current stream). `torch_gpu` times Popcorn's PyTorch reference
 (the `torch` implementation its dispatcher always holds, restated in
-popcorn_amd.compat.references) on the host's cores over a bounded row sample
-of the same workload. `others` holds the remaining configs' kernel figures.
+popcorn_amd.compat.references) on the same GPU and inputs: the competitor the
+record-driven selector compares against. `cpu_baseline` times that reference
+on the host's cores, on the full workload where it takes seconds and on a
+stated sample otherwise. `others` holds the same figures for the remaining
+configs, and `roofline_fractions` the dominant kernels' fractions of peak for
+C1-C5.
 """
 
 from __future__ import annotations
@@ -70,6 +74,7 @@ class Workload:
     launch: Callable[[int], None]  # one launch of the dominant kernel alone on input copy i
     config: dict = field(default_factory=dict)
     cpu: Callable[[], tuple[float, str]] | None = None  # -> (throughput in unit, sample description)
+    torch_step: Callable[[int], None] | None = None  # Popcorn's torch reference on the GPU, same inputs
 
 
 def _copies(nbytes: int) -> int:
@@ -83,6 +88,7 @@ def _randn(shape, dtype, gen, dev):
 
 def make_workload(name: str, dev: torch.device) -> Workload:
     from popcorn_amd import _lib, impls
+    from popcorn_amd.compat import references as R
 
     gen = torch.Generator(device=dev).manual_seed(0)
     lib = _lib.load()
@@ -104,16 +110,17 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                           1e-6, _lib.F32, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
             xc = torch.randn(rows, cols)
             wc = 1 + 0.1 * torch.randn(cols)
             t, reps = _time_cpu(lambda: R.rms_norm(xc, wc, None, 1e-6))
             return nbytes / t / 1e12, f"full C1 x [{rows}, {cols}] fp32, median of {reps} reps"
 
+        def torch_step(i):
+            R.rms_norm(xs[i % n], w, None, 1e-6)
+
         return Workload("c1", "RMSNorm forward fp32 x [4096, 4096]", "f32", "TB/s", nbytes, step,
                         "rmsnorm_fwd_grid", nbytes, launch,
-                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "fp32"}, cpu)
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "fp32"}, cpu, torch_step)
 
     if name == "c2":
         rows, cols = 16384, 14336
@@ -130,16 +137,17 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             _lib.check(lib.pk_swiglu_fwd(a.data_ptr(), b.data_ptr(), y.data_ptr(), numel, _lib.BF16, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            sample_rows = 1024
-            ac = torch.randn(sample_rows, cols).bfloat16()
-            bc = torch.randn(sample_rows, cols).bfloat16()
+            ac = torch.randn(rows, cols).bfloat16()
+            bc = torch.randn(rows, cols).bfloat16()
             t, reps = _time_cpu(lambda: R.swiglu(ac, bc))
-            return 3 * sample_rows * cols * 2 / t / 1e12, f"{sample_rows} of {rows} rows x {cols} bf16, median of {reps} reps"
+            return nbytes / t / 1e12, f"full C2 a, b [{rows}, {cols}] bf16, median of {reps} reps"
+
+        def torch_step(i):
+            R.swiglu(a, b)
 
         return Workload("c2", "SwiGLU forward bf16 a, b [16384, 14336]", "bf16", "TB/s", nbytes, step,
-                        "swiglu_fwd_vec", nbytes, launch, {"rows": rows, "cols": cols, "dtype": "bf16"}, cpu)
+                        "swiglu_fwd_vec", nbytes, launch, {"rows": rows, "cols": cols, "dtype": "bf16"}, cpu,
+                        torch_step)
 
     if name == "c3":
         B, S, HQ, HKV, D, half = 8, 4096, 32, 8, 128, 64
@@ -167,20 +175,20 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             rot(q, yq)
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            sb = 1
-            qc = torch.randn(sb, S, HQ, D).bfloat16()
-            kc = torch.randn(sb, S, HKV, D).bfloat16()
+            qc = torch.randn(B, S, HQ, D).bfloat16()
+            kc = torch.randn(B, S, HKV, D).bfloat16()
             cc, sc = cos.cpu(), sin.cpu()
             t, reps = _time_cpu(lambda: (R.rotary_embedding(qc, cc, sc), R.rotary_embedding(kc, cc, sc)))
-            work = 2 * (qc.numel() + kc.numel()) * 2 + 2 * table
-            return work / t / 1e12, f"batch 1 of {B} (q and k calls), median of {reps} reps"
+            return nbytes / t / 1e12, f"full C3 (q and k calls, fp32 tables), median of {reps} reps"
+
+        def torch_step(i):
+            R.rotary_embedding(q, cos, sin)
+            R.rotary_embedding(k, cos, sin)
 
         return Workload("c3", "Rotary NeoX bf16 q [8,4096,32,128] + k [8,4096,8,128], fp32 cos/sin [4096,64]",
                         "bf16", "TB/s", nbytes, step, "rotary_kernel", 2 * qb + table, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "theta": 500000.0,
-                         "dtype": "bf16", "tables": "fp32"}, cpu)
+                         "dtype": "bf16", "tables": "fp32"}, cpu, torch_step)
 
     if name == "rope":
         # not a BASELINE config: paired q/k rope at the shape of the notebook's fused qk-norm+rope example
@@ -210,25 +218,27 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                    yk.data_ptr(), strides, B, HQ, HKV, S, D, 1, _lib.BF16, _lib.BF16, 0, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            qc = torch.randn(1, HQ, S, D).bfloat16().requires_grad_()
-            kc = torch.randn(1, HKV, S, D).bfloat16().requires_grad_()
+            qc = torch.randn(B, HQ, S, D).bfloat16().requires_grad_()
+            kc = torch.randn(B, HKV, S, D).bfloat16().requires_grad_()
             cc, sc = cos.cpu(), sin.cpu()
-            gqc, gkc = torch.randn(1, HQ, S, D).bfloat16(), torch.randn(1, HKV, S, D).bfloat16()
+            gqc, gkc = torch.randn(B, HQ, S, D).bfloat16(), torch.randn(B, HKV, S, D).bfloat16()
 
             def one():
                 oq, ok = R.rope(qc, kc, cc, sc)
                 torch.autograd.grad((oq, ok), (qc, kc), (gqc, gkc))
 
             t, reps = _time_cpu(one)
-            work = 2 * (2 * (qc.numel() + kc.numel()) * 2 + 2 * S * D * 2)
-            return work / t / 1e12, f"batch 1 of {B}, fwd+bwd, median of {reps} reps"
+            return 2 * launch_bytes / t / 1e12, f"full shape, fwd+bwd, median of {reps} reps"
+
+        def torch_step(i):
+            q, k = leaves[i % n]
+            oq, ok = R.rope(q, k, cos, sin)
+            torch.autograd.grad((oq, ok), (q, k), (gq, gk))
 
         return Workload("rope", "rope fwd+bwd bf16 q [4,32,4096,128], k [4,8,4096,128], bf16 cos/sin [1,4096,128]",
                         "bf16", "TB/s", 2 * launch_bytes, step, "rope_kernel", launch_bytes, launch,
                         {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
-                         "theta": 500000.0, "dtype": "bf16"}, cpu)
+                         "theta": 500000.0, "dtype": "bf16"}, cpu, torch_step)
 
     if name == "qk_norm_rope":
         # not a BASELINE config: the kernel-writing notebook's fused op at its benchmark shape
@@ -269,28 +279,28 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                                _lib.BF16, _lib.BF16, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            qc = torch.randn(1, HQ, S, D).bfloat16().requires_grad_()
-            kc = torch.randn(1, HKV, S, D).bfloat16().requires_grad_()
+            qc = torch.randn(B, HQ, S, D).bfloat16().requires_grad_()
+            kc = torch.randn(B, HKV, S, D).bfloat16().requires_grad_()
             wq, wk = (torch.randn(D).bfloat16().requires_grad_() for _ in range(2))
             cc, sc = cos.cpu(), sin.cpu()
-            gqc, gkc = torch.randn(1, HQ, S, D).bfloat16(), torch.randn(1, HKV, S, D).bfloat16()
+            gqc, gkc = torch.randn(B, HQ, S, D).bfloat16(), torch.randn(B, HKV, S, D).bfloat16()
 
             def one():
                 oq, ok = R.qk_norm_rope(qc, kc, wq, wk, cc, sc, 1e-6)
                 torch.autograd.grad((oq, ok), (qc, kc, wq, wk), (gqc, gkc))
 
             t, reps = _time_cpu(one)
-            qk1 = (qc.numel() + kc.numel()) * 2
-            work = 5 * qk1 + 2 * (2 * S * D * 2 + 2 * D * 2 + 4 * (HQ + HKV) * S)
-            return work / t / 1e12, f"batch 1 of {B}, fwd+bwd, median of {reps} reps"
+            return (fwd_bytes + bwd_bytes) / t / 1e12, f"full shape, fwd+bwd, median of {reps} reps"
+
+        def torch_step(i):
+            oq, ok = R.qk_norm_rope(*leaves, cos, sin, 1e-6)
+            torch.autograd.grad((oq, ok), leaves, (gq, gk))
 
         return Workload("qk_norm_rope", "qk_norm_rope fwd+bwd bf16 q [4,32,4096,128], k [4,8,4096,128], "
                         "weights [128], bf16 cos/sin [1,4096,128]", "bf16", "TB/s", fwd_bytes + bwd_bytes, step,
                         "qk_norm_rope_bwd_kernel", bwd_bytes, launch,
                         {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
-                         "eps": 1e-6, "dtype": "bf16"}, cpu)
+                         "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step)
 
     if name == "c4":
         rows, cols = 65536, 8192
@@ -321,9 +331,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                           stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            sample = 2048
+            sample = rows
             xc = torch.randn(sample, cols).bfloat16().requires_grad_()
             wc = (1 + 0.1 * torch.randn(cols)).bfloat16().requires_grad_()
             gc = torch.randn(sample, cols).bfloat16()
@@ -333,12 +341,15 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                 torch.autograd.grad(yc, (xc, wc), gc)
 
             t, reps = _time_cpu(one)
-            work = 5 * sample * cols * 2 + 2 * cols * 2 + cols * 4
-            return work / t / 1e12, f"{sample} of {rows} rows x {cols} bf16, fwd+bwd, median of {reps} reps"
+            return (fwd_bytes + bwd_bytes) / t / 1e12, f"full C4 [{rows}, {cols}] bf16 fwd+bwd, median of {reps} reps"
+
+        def torch_step(i):
+            yy = R.rms_norm(xg, wg, None, 1e-6)
+            torch.autograd.grad(yy, (xg, wg), dy)
 
         return Workload("c4", "RMSNorm fwd+bwd bf16 x, dy [65536, 8192]", "bf16", "TB/s", fwd_bytes + bwd_bytes,
                         step, "rmsnorm_bwd_vec", bwd_bytes, launch,
-                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu)
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step)
 
     if name == "add_rmsnorm":
         # not a BASELINE config: the next op on the norm path (residual add + RMSNorm) at C4's shape
@@ -370,9 +381,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                               rows, cols, 1.0, _lib.BF16, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
-            sample = 2048
+            sample = rows
             xc, rc = (torch.randn(sample, cols).bfloat16().requires_grad_() for _ in range(2))
             wc = (1 + 0.1 * torch.randn(cols)).bfloat16().requires_grad_()
             gc, sc = torch.randn(sample, cols).bfloat16(), torch.randn(sample, cols).bfloat16()
@@ -382,12 +391,15 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                 torch.autograd.grad((yc, s_c), (xc, rc, wc), (gc, sc))
 
             t, reps = _time_cpu(one)
-            work = 8 * sample * cols * 2 + 2 * cols * 2 + cols * 4
-            return work / t / 1e12, f"{sample} of {rows} rows x {cols} bf16, fwd+bwd, median of {reps} reps"
+            return (fwd_bytes + bwd_bytes) / t / 1e12, f"full [{rows}, {cols}] bf16 fwd+bwd, median of {reps} reps"
+
+        def torch_step(i):
+            yy, ss = R.add_rms_norm(xg, rg, wg, 1e-6, 1.0)
+            torch.autograd.grad((yy, ss), (xg, rg, wg), (dy, ds))
 
         return Workload("add_rmsnorm", "add_rms_norm fwd+bwd bf16 x, residual, dy, ds [65536, 8192], offset 1",
                         "bf16", "TB/s", fwd_bytes + bwd_bytes, step, "rmsnorm_bwd_vec", bwd_bytes, launch,
-                        {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu)
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu, torch_step)
 
     if name == "attn_bwd":
         # not a BASELINE config: attention forward + backward at C5's shape (bf16, causal)
@@ -415,8 +427,6 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                        strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
-
             sq = 1024  # one (batch, kv group) of 1024 tokens; work scaled to that
             qc = torch.randn(1, sq, 4, D).bfloat16().requires_grad_()
             kc, vc = (torch.randn(1, sq, 1, D).bfloat16().requires_grad_() for _ in range(2))
@@ -430,10 +440,14 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             work = 3.5 * 4.0 * 4 * D * sq * sq / 2
             return work / t / 1e12, f"B=1, S={sq}, Hq=4, Hkv=1 causal fwd+bwd bf16, median of {reps} reps"
 
+        def torch_step(i):
+            out = R.attn(qg, kg, vg, True)
+            torch.autograd.grad(out, (qg, kg, vg), do)
+
         return Workload("attn_bwd", "Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16",
                         "TFLOP/s", fwd_flops + bwd_flops, step, "attn_bwd", bwd_flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
-                         "dtype": "bf16"}, cpu)
+                         "dtype": "bf16"}, cpu, torch_step)
 
     if name == "c5":
         B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
@@ -454,20 +468,35 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                        strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
 
         def cpu():
-            from popcorn_amd.compat import references as R
+            # The largest of (B, S) = (1, 2048), (1, 4096), (1, 8192), (4, 8192) -- the last is C5
+            # itself -- whose warmup plus two timed reps fit about 30 s on this host, estimated
+            # from (1, 2048).
+            def sample(b_cpu, s_cpu):
+                qc = torch.randn(b_cpu, s_cpu, HQ, D).bfloat16()
+                kc, vc = (torch.randn(b_cpu, s_cpu, HKV, D).bfloat16() for _ in range(2))
+                return lambda: R.attn(qc, kc, vc, True)
 
-            s_cpu = 2048
-            qc = torch.randn(1, s_cpu, HQ, D).bfloat16()
-            kc = torch.randn(1, s_cpu, HKV, D).bfloat16()
-            vc = torch.randn(1, s_cpu, HKV, D).bfloat16()
-            t, reps = _time_cpu(lambda: R.attn(qc, kc, vc, True), min_reps=2)
-            work = 4.0 * HQ * D * s_cpu * s_cpu / 2
-            return work / t / 1e12, f"B=1, S={s_cpu} (of B=4, S=8192), causal, median of {reps} reps"
+            probe = sample(1, 2048)
+            probe()
+            t0 = time.perf_counter()
+            probe()
+            unit = time.perf_counter() - t0
+            fits = [(b_, s_) for b_, s_ in ((1, 2048), (1, 4096), (1, 8192), (4, 8192))
+                    if 3 * unit * b_ * (s_ / 2048) ** 2 <= 30.0]
+            b_cpu, s_cpu = fits[-1] if fits else (1, 2048)
+            t, reps = _time_cpu(sample(b_cpu, s_cpu), budget_s=0.0, min_reps=2, max_reps=2)
+            work = 4.0 * b_cpu * HQ * D * s_cpu * s_cpu / 2
+            what = "full C5" if (b_cpu, s_cpu) == (B, S) else f"B={b_cpu}, S={s_cpu} of C5's B=4, S=8192"
+            return work / t / 1e12, f"{what}, causal bf16, 1 warmup + median of {reps} reps"
+
+        def torch_step(i):
+            with torch.no_grad():
+                R.attn(q, k, v, True)
 
         return Workload("c5", "Causal GQA attention fwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16", "TFLOP/s",
                         flops, step, "attn_fwd_kernel", flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
-                         "dtype": "bf16"}, cpu)
+                         "dtype": "bf16"}, cpu, torch_step)
 
     if name == "copy":
         numel = 256 << 20  # 512 MiB of bf16 each way
@@ -484,7 +513,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
     raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, attn_bwd, copy)")
 
 
-def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 20) -> tuple[float, int]:
+def _time_cpu(fn, budget_s: float = 5.0, min_reps: int = 2, max_reps: int = 20) -> tuple[float, int]:
     """Median wall time of fn on the CPU after one warmup, over reps filling about budget_s."""
     t0 = time.perf_counter()
     fn()
@@ -538,18 +567,37 @@ def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
     }
 
 
-def _cpu_baseline(wl: Workload) -> dict | None:
-    if wl.cpu is None:
-        return None
+def _cpu_threads() -> tuple[int, int]:
+    """(threads to use, cores this process may run on): every core of the affinity mask, within the
+    host's CPU share for this GPU when one is set (OMP_NUM_THREADS on the GPU boxes)."""
     try:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
         affinity = os.cpu_count() or 1
-    threads = max(1, min(affinity, 16))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(affinity, share) if share > 0 else affinity), affinity
+
+
+def _cpu_baseline(wl: Workload) -> dict | None:
+    if wl.cpu is None:
+        return None
+    threads, affinity = _cpu_threads()
     torch.set_num_threads(threads)
     value, sample = wl.cpu()
     return {"value": round(value, 6), "unit": wl.unit, "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"popcorn reference (torch, CPU): {sample}; host os.cpu_count()={os.cpu_count()}"}
+            "sample": f"popcorn reference (torch, CPU): {sample}; {torch.get_num_threads()} threads, affinity "
+                      f"{affinity} cores, os.cpu_count()={os.cpu_count()}"}
+
+
+def _torch_on_gpu(wl: Workload, ours_ms: float, steps: int, warmup: int) -> dict | None:
+    """Popcorn's torch reference timed on the same device and inputs: the implementation the selector
+    compares against."""
+    if wl.torch_step is None:
+        return None
+    total, _ = _time_gpu(wl.torch_step, steps, warmup)
+    per = total / steps
+    return {"ms_per_step": round(per, 4), "value": round(_rate(wl.work, per, wl.unit), 4),
+            "speedup": round(per / ours_ms, 3)}
 
 
 def main(argv=None) -> int:
@@ -584,31 +632,41 @@ def main(argv=None) -> int:
     roof = _roofline(wl, args.steps, args.warmup)
     print(f"bench: {wl.kernel} {roof['avg_launch_us']} us/launch, frac {roof['frac']}", file=sys.stderr, flush=True)
 
+    torch_gpu = _torch_on_gpu(wl, ms_per_step, args.steps, args.warmup)
+    if torch_gpu:
+        print(f"bench: torch on the GPU {torch_gpu['ms_per_step']} ms/step ({torch_gpu['speedup']}x)", file=sys.stderr,
+              flush=True)
+    cpu = None if args.no_cpu else _cpu_baseline(wl)
+
+    head_unit, head_dtype, head_config = wl.unit, wl.dtype, {"workload": wl.description, **wl.config}
     others = {}
     if not args.no_others and wl.name != "copy":
+        del wl
         for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope"):
-            if name == wl.name:
+            if name == args.workload:
                 continue
-            del wl
             torch.cuda.empty_cache()
             wl_o = make_workload(name, dev)
-            tot, _ = _time_gpu(wl_o.step, max(5, args.steps // 2), 2)
-            per = tot / max(5, args.steps // 2)
-            r = _roofline(wl_o, max(5, args.steps // 2), 2)
-            others[name] = {"workload": wl_o.description, "ms_per_step": round(per, 4),
-                            "value": round(_rate(wl_o.work, per, wl_o.unit), 4), "unit": wl_o.unit,
-                            "roofline": r}
-            print(f"bench: {name} {per:.4f} ms/step; {r['kernel']} frac {r['frac']}", file=sys.stderr, flush=True)
-            wl = wl_o
-        del wl
+            reps = max(5, args.steps // 2)
+            tot, _ = _time_gpu(wl_o.step, reps, 2)
+            per = tot / reps
+            entry = {"workload": wl_o.description, "ms_per_step": round(per, 4),
+                     "value": round(_rate(wl_o.work, per, wl_o.unit), 4), "unit": wl_o.unit,
+                     "roofline": _roofline(wl_o, reps, 2), "torch_gpu": _torch_on_gpu(wl_o, per, reps, 2)}
+            if not args.no_cpu:
+                entry["cpu_baseline"] = _cpu_baseline(wl_o)
+            others[name] = entry
+            print(f"bench: {name} {per:.4f} ms/step; {entry['roofline']['kernel']} frac {entry['roofline']['frac']}"
+                  + (f"; torch {entry['torch_gpu']['ms_per_step']} ms" if entry["torch_gpu"] else ""),
+                  file=sys.stderr, flush=True)
+            del wl_o
         torch.cuda.empty_cache()
-        wl = make_workload(args.workload, dev)
 
-    cpu = None if args.no_cpu else _cpu_baseline(wl)
+    fractions = {args.workload: roof["frac"], **{name: o["roofline"]["frac"] for name, o in others.items()}}
     line = {
         "metric": METRIC,
         "value": round(value, 4),
-        "unit": wl.unit,
+        "unit": head_unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -616,11 +674,13 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": wl.dtype,
+        "dtype": head_dtype,
         "data": "synthetic N(0,1) inputs, seeded device generator, resident in HBM",
-        "config": {"workload": wl.description, **wl.config},
+        "config": head_config,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "torch_gpu": torch_gpu,
+        "roofline_fractions": {name: fractions[name] for name in ("c1", "c2", "c3", "c4", "c5") if name in fractions},
         "others": others,
     }
     print(json.dumps(line), flush=True)

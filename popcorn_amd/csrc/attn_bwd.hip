@@ -258,6 +258,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[1][dt] + 16 * c * L::ST));
         return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       };
+      static_assert(RING <= NSC && NSC + RING <= NALL, "ring reads stay inside the run");
       Frag ring[RING];
 #pragma unroll
       for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
@@ -492,6 +493,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[1][dt] + 16 * c * L::ST));
       return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
+    static_assert(RING <= 2 * KK, "the ring's first reads stay inside the run");
     Frag ring[RING];
 #pragma unroll
     for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
@@ -501,7 +503,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 #pragma unroll
     for (int i = 0; i < KK; ++i) {
       const Frag f = ring[i % RING];
-      ring[i % RING] = fetch(i + RING);
+      if (i + RING < 2 * KK) ring[i % RING] = fetch(i + RING);  // at head_dim 64 the run is only 8 long
       sres = Mma<T>::run(f, bf[i], sres);
       __builtin_amdgcn_sched_barrier(0);
     }

@@ -185,3 +185,71 @@ def test_attn_bwd_rejects_a_short_workspace():
                          ws.data_ptr(), need - 1, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), st, b, s, hq, hkv, d,
                          d**-0.5, 1, _lib.BF16, _lib.stream_handle(q.device))
     assert rc != 0 and b"workspace" in lib.pk_last_error()
+
+
+# --------------------------------------------------------------------------- dk/dv launch paths
+# The dk/dv kernel walks every q head of its kv group in one block (the direct
+# path, nsplit = 1) when the grid of 128-key blocks fills the device twice
+# over; otherwise it splits the group's q heads over nsplit blocks that leave
+# fp32 partials. These cases pin each path on full-size grids, checking
+# sampled (batch, kv group) slices against the float64 oracle: a kv group's
+# gradients depend only on its own q heads, so a slice is an exact subproblem.
+
+
+def _splits(ws_bytes, lse_n, rows, hkv, d):
+    lse = -(-2 * lse_n * 4 // 256) * 256
+    return (ws_bytes - lse) // (2 * rows * hkv * d * 4) if ws_bytes > lse else 1
+
+
+def _check_group_slices(q, k, v, do, grads, causal, dtype, picks, what):
+    group = q.shape[2] // k.shape[2]
+    for b, g in picks:
+        heads = slice(g * group, (g + 1) * group)
+        qs, ks, vs, dos = q[b:b + 1, :, heads], k[b:b + 1, :, g:g + 1], v[b:b + 1, :, g:g + 1], do[b:b + 1, :, heads]
+        truth = O.attention_bwd(*(t.double().cpu().numpy() for t in (qs, ks, vs, dos)), causal, None)
+        _, ref = _grads(lambda a, c, e: R.attn(a, c, e, causal, None), [t.cpu() for t in (qs, ks, vs)], dos.cpu())
+        mine = (grads[0][b:b + 1, :, heads], grads[1][b:b + 1, :, g:g + 1], grads[2][b:b + 1, :, g:g + 1])
+        for name, got, want, r in zip(("dq", "dk", "dv"), mine, truth, ref):
+            gauge_ok(got, want, r, dtype, f"{name} ({what}, batch {b}, kv group {g})")
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,d,dtype,causal,splits", [
+    (4, 1024, 32, 16, 64, torch.bfloat16, True, 1),    # 512 blocks: direct, two q heads per block
+    (8, 1024, 32, 8, 128, torch.float16, False, 1),    # 512 blocks: direct, four q heads per block
+    (4, 1024, 32, 8, 64, torch.bfloat16, False, 2),    # 256 blocks: two splits of two q heads
+    (4, 1024, 32, 8, 128, torch.float16, True, 2),
+    (2, 1024, 64, 8, 128, torch.bfloat16, True, 4),    # 128 blocks, group 8: four splits of two heads
+], ids=["direct-d64-bf16-causal", "direct-d128-fp16-full", "split2-d64-bf16-full", "split2-d128-fp16-causal",
+        "split4of8-d128-bf16-causal"])
+def test_attn_bwd_dkdv_direct_and_partial_splits(b, s, hq, hkv, d, dtype, causal, splits):
+    lib = _lib.load()
+    assert _splits(lib.pk_attn_bwd_workspace(b, s, hq, hkv, d), b * hq * s, b * s, hkv, d) == splits
+    gen = torch.Generator(device=DEV).manual_seed(17)
+    q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    k, v = (torch.randn(b, s, hkv, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    grads = torch.autograd.grad(impls.attn(*leaves, causal), leaves, do)
+    _check_group_slices(q, k, v, do, grads, causal, dtype, [(0, 0), (b - 1, hkv - 1)], f"{splits} split(s)")
+
+
+@pytest.mark.parametrize("seqs,length,splits", [(8, 1024, 1), (4, 1024, 2)], ids=["direct", "split2"])
+def test_attn_varlen_bwd_dkdv_direct_and_partial_splits(seqs, length, splits):
+    """Packed sequences write dk/dv directly into their token rows, or sum partials per token."""
+    hq, hkv, d, dtype = 32, 8, 128, torch.bfloat16
+    lens = [length - 37 * i for i in range(seqs)]  # ragged, the longest sizes the grid
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    total = int(cu[-1])
+    lib = _lib.load()
+    ws = lib.pk_attn_varlen_bwd_workspace(seqs, total, max(lens), hq, hkv, d)
+    assert _splits(ws, hq * total, total, hkv, d) == splits
+    gen = torch.Generator(device=DEV).manual_seed(23)
+    q, do = (torch.randn(total, hq, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    k, v = (torch.randn(total, hkv, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    grads = torch.autograd.grad(impls.attn_varlen(*leaves, cu.to(DEV), True), leaves, do)
+    for seg in (0, seqs - 1):
+        rows = slice(int(cu[seg]), int(cu[seg + 1]))
+        seg_view = [t[rows].unsqueeze(0) for t in (q, k, v, do)]
+        seg_grads = [g[rows].unsqueeze(0) for g in grads]
+        _check_group_slices(*seg_view, seg_grads, True, dtype, [(0, 0), (0, hkv - 1)],
+                            f"varlen {splits} split(s), sequence {seg}")
