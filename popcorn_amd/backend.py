@@ -11,10 +11,10 @@ op (core/dispatcher.py:324-345), exactly what a backend module under
 `popcorn_amd.impls` functions already carry the reference signatures, so
 Popcorn calls them directly (core/dispatcher.py:184-201).
 
-The backend's distribution is `popcorn-amd` at `popcorn_amd.__version__`,
-pinned as both bounds of the version gate; its metadata sits next to the
-package (`popcorn_amd-<version>.dist-info`), so the gate resolves whenever
-the repository root is on `sys.path`, with or without a pip install.
+The backend's distribution is `popcorn-amd` at `popcorn_amd.__version__`
+(setup.py), pinned as both bounds of the version gate; the gate resolves for
+an installed copy, and in a source tree once `popcorn_amd.build.build()` has
+written the metadata beside the package.
 
 The predicates only describe what the kernels cover -- tensors on a HIP
 device, one floating dtype per call, the shapes the kernels implement.

@@ -2,7 +2,10 @@
 
 `python -m popcorn_amd.build` compiles every `csrc/*.hip` to an object in
 `popcorn_amd/_build/` (in parallel) and links `popcorn_amd/libpopcorn_amd.so`.
-The library is always rebuilt: the call is the "does it build" check.
+The library is always rebuilt: the call is the "does it build" check. In a
+source tree it then writes the `popcorn-amd` distribution metadata beside the
+package (setup.py's `egg_info`, as an editable install would), so Popcorn's
+version gate sees the backend when the tree itself is on `sys.path`.
 """
 
 from __future__ import annotations
@@ -73,7 +76,19 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
+    write_metadata()
     return LIBRARY
+
+
+def write_metadata() -> None:
+    """Run setup.py's `egg_info` in a source tree (no-op for an installed package, which has its metadata)."""
+    setup_py = PACKAGE.parent / "setup.py"
+    if not setup_py.exists():
+        return
+    proc = subprocess.run([sys.executable, str(setup_py), "-q", "egg_info", "--egg-base", str(PACKAGE.parent)],
+                          cwd=PACKAGE.parent, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"writing the popcorn-amd metadata failed:\n{proc.stderr}")
 
 
 if __name__ == "__main__":
