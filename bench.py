@@ -107,7 +107,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
 
         def launch(i):
             _lib.check(lib.pk_rmsnorm_fwd(xs[i % n].data_ptr(), w.data_ptr(), None, y.data_ptr(), None, rows, cols,
-                                          1e-6, _lib.F32, stream()))
+                                          1e-6, _lib.F32, _lib.F32, stream()))
 
         def cpu():
             xc = torch.randn(rows, cols)
@@ -215,7 +215,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         def launch(i):
             q, k = qs[i % n], ks[i % n]
             _lib.check(lib.pk_rope(q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(), yq.data_ptr(),
-                                   yk.data_ptr(), strides, B, HQ, HKV, S, D, 1, _lib.BF16, _lib.BF16, 0, stream()))
+                                   yk.data_ptr(), strides, B, HQ, HKV, S, D, 1, _lib.BF16, _lib.BF16, _lib.BF16, 0,
+                                   stream()))
 
         def cpu():
             qc = torch.randn(B, HQ, S, D).bfloat16().requires_grad_()
@@ -262,7 +263,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         st12 = (_lib._i64 * 12)(*(x for t in (q, k, yq, yk) for x in t.stride()[:3]))
         _lib.check(lib.pk_qk_norm_rope_fwd(q.data_ptr(), k.data_ptr(), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
                                            sin.data_ptr(), yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(),
-                                           st12, B, HQ, HKV, S, D, 1, 1e-6, _lib.BF16, _lib.BF16, stream()))
+                                           st12, B, HQ, HKV, S, D, 1, 1e-6, _lib.BF16, _lib.BF16, _lib.BF16,
+                                           stream()))
         ws_bytes = lib.pk_qk_norm_rope_bwd_workspace(B, HQ, HKV, S, D, _lib.BF16)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         st18 = (_lib._i64 * 18)(*(x for t in (q, k, gq, gk, dq, dk) for x in t.stride()[:3]))
@@ -276,7 +278,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                                cos.data_ptr(), sin.data_ptr(), rq.data_ptr(), rk.data_ptr(),
                                                gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                                                dw.data_ptr(), ws.data_ptr(), ws_bytes, st18, B, HQ, HKV, S, D, 1,
-                                               _lib.BF16, _lib.BF16, stream()))
+                                               _lib.BF16, _lib.BF16, _lib.BF16, stream()))
 
         def cpu():
             qc = torch.randn(B, HQ, S, D).bfloat16().requires_grad_()
@@ -317,7 +319,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         dw = torch.empty_like(w)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         _lib.check(lib.pk_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), None, y.data_ptr(), rstd.data_ptr(), rows, cols,
-                                      1e-6, _lib.BF16, stream()))
+                                      1e-6, _lib.BF16, _lib.BF16, stream()))
         ws_bytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, _lib.BF16)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
@@ -328,7 +330,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         def launch(i):
             _lib.check(lib.pk_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(), dx.data_ptr(),
                                           dw.data_ptr(), None, ws.data_ptr(), ws_bytes, rows, cols, _lib.BF16,
-                                          stream()))
+                                          _lib.BF16, stream()))
 
         def cpu():
             sample = rows

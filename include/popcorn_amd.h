@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 3
+#define PK_ABI_VERSION 4
 
 /* status codes */
 #define PK_OK 0
@@ -62,28 +62,33 @@ int pk_swiglu_bwd(const void* dy, const void* a, const void* b, void* da, void* 
 
 /*
  * RMSNorm forward over `rows` contiguous rows of `cols` elements:
- *   r = 1/sqrt(mean(x^2) + eps); y = round(round(x*r) * w) [+ bias].
- * x, w, bias and y share `dtype`; bias may be NULL; rstd (fp32 [rows]) may be
- * NULL and otherwise receives r for the backward pass.
+ *   r = 1/sqrt(mean(x^2) + eps); n = round_x(x*r); y = n * w [+ bias],
+ * each product and sum rounded to w_dtype. x has `dtype`; w, bias and y have
+ * `w_dtype`, which is `dtype`, or PK_F32 with a 16-bit x (torch promotes a
+ * 16-bit normalised row times an fp32 weight to fp32). bias may be NULL;
+ * rstd (fp32 [rows]) may be NULL and otherwise receives r for the backward.
  * Replaces: reference `rms_norm` (kernels/rms_norm.py:16-30) with `rms`
  * (kernels/_utils.py:14-16).
  */
 int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, float* rstd, int64_t rows, int64_t cols,
-                   float eps, int dtype, void* stream);
+                   float eps, int dtype, int w_dtype, void* stream);
 
-/* Bytes of device workspace pk_rmsnorm_bwd and pk_add_rmsnorm_bwd need for this shape. */
+/* Bytes of device workspace pk_rmsnorm_bwd and pk_add_rmsnorm_bwd need for rows of
+   x dtype `dtype` (any weight dtype). */
 int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
 
 /*
  * RMSNorm backward. With n = x*r and u = dy*w:
  *   dx = r*(u - n*mean(u*n)), dw = sum_rows dy*n, dbias = sum_rows dy.
  * Accumulation is fp32 and deterministic (per-block partial rows in
- * `workspace`, then one column reduction); dw and dbias are rounded once to
- * `dtype`. dbias may be NULL. rstd is the forward's output.
+ * `workspace`, then one column reduction). x and dx have `dtype`; w, dy, dw
+ * and dbias have `w_dtype` (as pk_rmsnorm_fwd); dw and dbias are rounded once.
+ * dbias may be NULL. rstd is the forward's output.
  * Replaces torch autograd of the reference (kernels/rms_norm.py:29-30).
  */
 int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
-                   void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream);
+                   void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, int w_dtype,
+                   void* stream);
 
 /*
  * pk_rmsnorm_bwd without a workspace argument and without any allocation:
@@ -101,7 +106,7 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
  * that forbid hipMalloc).
  */
 int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw,
-                           void* dbias, int64_t rows, int64_t cols, int dtype, void* stream);
+                           void* dbias, int64_t rows, int64_t cols, int dtype, int w_dtype, void* stream);
 
 /*
  * Residual add fused with RMSNorm, over `rows` contiguous rows of `cols`:
@@ -146,15 +151,19 @@ int pk_rotary(const void* x, const void* cos, const void* sin, void* y, const in
  * cos, sin [cos_batch, seq, head_dim] (contiguous; cos_batch 1 or batch):
  *   y[j] = x[j] cos[j] - x[j+h] sin[j],  y[j+h] = x[j+h] cos[j+h] + x[j] sin[j+h]
  * (h = head_dim/2), i.e. x*cos + rotate_half(x)*sin, fp32 arithmetic rounded
- * once to x's dtype. transpose = 1 applies the adjoint map (the backward):
+ * once to y_dtype. transpose = 1 applies the adjoint map (the backward):
  *   dx[j] = g[j] cos[j] + g[j+h] sin[j+h],  dx[j+h] = g[j+h] cos[j+h] - g[j] sin[j].
- * strides[12] = q, k, yq, yk (batch, head, seq) strides in elements; the
- * last dimension is contiguous. A side with zero heads may pass NULL.
+ * x_dtype is what is read (q, k, or the cotangents), y_dtype what is written:
+ * one dtype, or a 16-bit one with PK_F32 either way (16-bit q/k times fp32
+ * tables promote to fp32 outputs; their backward reads fp32 cotangents and
+ * writes 16-bit gradients). strides[12] = q, k, yq, yk (batch, head, seq)
+ * strides in elements; the last dimension is contiguous. A side with zero
+ * heads may pass NULL.
  * Replaces: reference `rope` (kernels/rope.py:19-36).
  */
 int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void* yq, void* yk,
             const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-            int64_t cos_batch, int x_dtype, int cs_dtype, int transpose, void* stream);
+            int64_t cos_batch, int x_dtype, int y_dtype, int cs_dtype, int transpose, void* stream);
 
 /*
  * Per-head RMSNorm of q and k followed by pk_rope's rotation, in one pass
@@ -162,7 +171,9 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
  *   r = 1/sqrt(mean(x^2) + eps) over head_dim,  n = x*r*w,
  *   y = n*cos + rotate_half(n)*sin,
  * with w = q_weight [head_dim] for q rows and k_weight for k rows. fp32
- * arithmetic, one rounding per output. rstd_q [batch, q_heads, seq] and
+ * arithmetic, one rounding per output, to y_dtype: x_dtype, or PK_F32 with
+ * 16-bit inputs (fp32 tables promote the reference's rotation to fp32).
+ * rstd_q [batch, q_heads, seq] and
  * rstd_k [batch, kv_heads, seq] (fp32) receive r for the backward.
  * strides[12] = q, k, yq, yk (batch, head, seq) strides in elements, all
  * multiples of the 16-byte pack (8 bf16/fp16, 4 fp32); the last dimension is
@@ -176,7 +187,7 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
 int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
                         const void* sin, void* yq, void* yk, float* rstd_q, float* rstd_k, const int64_t* strides,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-                        int64_t cos_batch, float eps, int x_dtype, int cs_dtype, void* stream);
+                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, void* stream);
 
 /* Bytes of device workspace pk_qk_norm_rope_bwd needs for this shape (-1 if unsupported). */
 int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
@@ -187,7 +198,8 @@ int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv
  *   g = rotation^T(dy),  u = g*w,  dx = r*(u - x*r^2*<u, x>/head_dim),
  *   dw = sum over rows of g*x*r.
  * dw is [2, head_dim] in x's dtype: row 0 the q_weight gradient, row 1 the
- * k_weight gradient, summed deterministically through the workspace.
+ * k_weight gradient, summed deterministically through the workspace. The
+ * cotangents dyq, dyk have dy_dtype (the forward's y_dtype); dq, dk x's.
  * strides[18] = q, k, dyq, dyk, dq, dk (batch, head, seq) strides.
  * Replaces: torch autograd of the notebook's reference; stands beside its
  * Triton `_bwd` (cell 9).
@@ -196,7 +208,7 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
                         const void* sin, const float* rstd_q, const float* rstd_k, const void* dyq, const void* dyk,
                         void* dq, void* dk, void* dw, void* workspace, int64_t workspace_bytes,
                         const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
-                        int64_t head_dim, int64_t cos_batch, int x_dtype, int cs_dtype, void* stream);
+                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, void* stream);
 
 /*
  * Attention forward, o = softmax(q k^T * scale + M) v, grouped-query:

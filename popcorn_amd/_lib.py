@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libpopcorn_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -31,17 +31,17 @@ SIGNATURES = {
     "pk_last_error": (ctypes.c_char_p, []),
     "pk_swiglu_fwd": (_int, [_p, _p, _p, _i64, _int, _p]),
     "pk_swiglu_bwd": (_int, [_p, _p, _p, _p, _p, _i64, _int, _p]),
-    "pk_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _f32, _int, _p]),
+    "pk_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _f32, _int, _int, _p]),
     "pk_rmsnorm_bwd_workspace": (_i64, [_i64, _i64, _int]),
-    "pk_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _p]),
-    "pk_rmsnorm_bwd_noalloc": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _int, _p]),
+    "pk_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _p]),
+    "pk_rmsnorm_bwd_noalloc": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
     "pk_add_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _int, _p]),
     "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _p]),
     "pk_rotary": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
-    "pk_rope": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _p]),
-    "pk_qk_norm_rope_fwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
+    "pk_rope": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
+    "pk_qk_norm_rope_fwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _int, _p]),
     "pk_qk_norm_rope_bwd_workspace": (_i64, [_i64, _i64, _i64, _i64, _i64, _int]),
-    "pk_qk_norm_rope_bwd": (_int, [_p] * 14 + [_i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _p]),
+    "pk_qk_norm_rope_bwd": (_int, [_p] * 14 + [_i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _p]),
     "pk_attn_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_attn_bwd_workspace": (_i64, [_i64] * 5),
     "pk_attn_bwd": (_int, [_p] * 7 + [_i64] + [_p] * 4 + [_i64] * 5 + [_f32, _int, _int, _p]),

@@ -46,14 +46,16 @@ def _on_hip(*tensors: Any) -> bool:
 
 
 _FLOATS = (torch.float32, torch.bfloat16, torch.float16)
+_HALF = (torch.bfloat16, torch.float16)
 
 
 def rms_norm_supported(x, weight, bias, eps) -> bool:
-    tensors = [t for t in (x, weight, bias) if t is not None]
+    """One float dtype, or a 16-bit x with fp32 weight and bias (the output promotes to fp32)."""
     return (
-        _on_hip(*tensors)
-        and len({t.dtype for t in tensors}) == 1
+        _on_hip(x, weight, bias)
         and x.dtype in _FLOATS
+        and (weight.dtype == x.dtype or (x.dtype in _HALF and weight.dtype == torch.float32))
+        and (bias is None or bias.dtype == weight.dtype)
         and x.shape[-1] > 0
     )
 
@@ -84,10 +86,13 @@ def rotary_supported(x, cos, sin, interleaved) -> bool:
 
 
 def rope_supported(q, k, cos, sin) -> bool:
+    """q, k one float dtype; cos, sin one float dtype (fp32 tables beside 16-bit q/k promote the outputs)."""
     return (
         _on_hip(q, k, cos, sin)
         and q.dtype in _FLOATS
-        and q.dtype == k.dtype == cos.dtype == sin.dtype
+        and q.dtype == k.dtype
+        and cos.dtype in _FLOATS
+        and cos.dtype == sin.dtype
         and q.dim() == k.dim() == 4
         and cos.dim() == 3
         and cos.shape == sin.shape
@@ -113,7 +118,9 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
     return (
         _on_hip(q, k, q_weight, k_weight, cos, sin)
         and q.dtype in _FLOATS
-        and q.dtype == k.dtype == q_weight.dtype == k_weight.dtype == cos.dtype == sin.dtype
+        and q.dtype == k.dtype == q_weight.dtype == k_weight.dtype
+        and cos.dtype in _FLOATS
+        and cos.dtype == sin.dtype
         and q.dim() == k.dim() == 4
         and cos.dim() == 3
         and cos.shape == sin.shape

@@ -57,6 +57,37 @@ template <typename T> __device__ __forceinline__ void st16_stream(T* p, const Ve
   __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&r), reinterpret_cast<u32x4*>(p));
 }
 
+// N elements of E whose bytes are a whole number of 16-byte vectors: the pack
+// of a wider type that lines up with one Vec of a narrower one (8 fp32 beside
+// 8 bf16 values, say), moved as one or more 16-byte accesses.
+template <typename E, int N> struct alignas(16) Lane {
+  static_assert(N * sizeof(E) % 16 == 0, "a lane pack is whole 16-byte vectors");
+  static constexpr int kVectors = N * (int)sizeof(E) / 16;
+  E v[N];
+};
+
+template <typename E, int N> __device__ __forceinline__ Lane<E, N> ld_lane(const E* p) {
+  Lane<E, N> r;
+#pragma unroll
+  for (int i = 0; i < Lane<E, N>::kVectors; ++i)
+    reinterpret_cast<uint4*>(r.v)[i] = reinterpret_cast<const uint4*>(p)[i];
+  return r;
+}
+
+template <typename E, int N> __device__ __forceinline__ Lane<E, N> ld_lane_stream(const E* p) {
+  Lane<E, N> r;
+#pragma unroll
+  for (int i = 0; i < Lane<E, N>::kVectors; ++i)
+    reinterpret_cast<u32x4*>(r.v)[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + i);
+  return r;
+}
+
+template <typename E, int N> __device__ __forceinline__ void st_lane_stream(E* p, const Lane<E, N>& r) {
+#pragma unroll
+  for (int i = 0; i < Lane<E, N>::kVectors; ++i)
+    __builtin_nontemporal_store(reinterpret_cast<const u32x4*>(r.v)[i], reinterpret_cast<u32x4*>(p) + i);
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

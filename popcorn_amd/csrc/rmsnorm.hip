@@ -21,6 +21,11 @@
 // Blocks leave one fp32 partial row each (the rows of a block's wavefront
 // slots are combined through LDS first), and a two-stage column reduction
 // sums the partials in a fixed order, so dw is deterministic.
+//
+// Types: T is x's type (and dx's); W is the weight's, which is also the type
+// of the bias, of y and of dy, and of dw / dbias: W = T, or fp32 with a 16-bit
+// x (torch's promotion of a 16-bit normalised row times an fp32 weight gives
+// an fp32 result, unrounded).
 #include <math.h>
 
 #include <mutex>
@@ -65,24 +70,26 @@ template <typename T> __device__ __forceinline__ void add_residual(Vec<T>& xv, c
 #pragma unroll
   for (int j = 0; j < Vec<T>::N; ++j) xv.v[j] = from_f32<T>(to_f32(xv.v[j]) + to_f32(rv.v[j]));
 }
-// w + offset, rounded to T like the reference's `weight + offset`
-template <typename T> __device__ __forceinline__ Vec<T> offset_weight(Vec<T> wv, float offset) {
+// w + offset, rounded to the weight's type like the reference's `weight + offset`
+template <typename W, int N> __device__ __forceinline__ Lane<W, N> offset_weight(Lane<W, N> wv, float offset) {
 #pragma unroll
-  for (int j = 0; j < Vec<T>::N; ++j) wv.v[j] = from_f32<T>(to_f32(wv.v[j]) + offset);
+  for (int j = 0; j < N; ++j) wv.v[j] = from_f32<W>(to_f32(wv.v[j]) + offset);
   return wv;
 }
 
-template <typename T, bool BIAS> __device__ __forceinline__ T fwd_elem(float xv, float r, float wv, float bv) {
+// torch: n = (h * r).to(T); y = n * w (at W); y = y + bias. With W = T every
+// op rounds to T; with W = fp32 only n is rounded.
+template <typename T, typename W, bool BIAS> __device__ __forceinline__ W fwd_elem(float xv, float r, float wv, float bv) {
   float y = round_to<T>(xv * r) * wv;
-  if constexpr (BIAS) y = round_to<T>(y) + bv;
-  return from_f32<T>(y);
+  if constexpr (BIAS) y = round_to<W>(y) + bv;
+  return from_f32<W>(y);
 }
 
 // One row per TPR lanes, RPB = NTB / TPR rows per block.
-template <typename T, int NTB, int TPR, int VPT, int MODE>
-__global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, const T* __restrict__ w,
-                                                       const T* __restrict__ bias, const T* __restrict__ res,
-                                                       T* __restrict__ s_out, float offset, T* __restrict__ y,
+template <typename T, typename W, int NTB, int TPR, int VPT, int MODE>
+__global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, const W* __restrict__ w,
+                                                       const W* __restrict__ bias, const T* __restrict__ res,
+                                                       T* __restrict__ s_out, float offset, W* __restrict__ y,
                                                        float* __restrict__ rstd, int64_t rows, int cols, float eps,
                                                        float inv_cols) {
   constexpr bool BIAS = MODE == kBias;
@@ -118,20 +125,20 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
   const float r = 1.0f / sqrtf(ss * inv_cols + eps);
   if (rstd != nullptr && lane == 0) rstd[row] = r;
 
-  T* yr = y + row * cols;
+  W* yr = y + row * cols;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     const int v = lane + k * TPR;
     if (v < nvec) {
-      Vec<T> wv = ld16(w + v * P);
+      Lane<W, P> wv = ld_lane<W, P>(w + v * P);
       if constexpr (MODE == kAdd) wv = offset_weight(wv, offset);
-      Vec<T> bv;
-      if constexpr (BIAS) bv = ld16(bias + v * P);
-      Vec<T> out;
+      Lane<W, P> bv;
+      if constexpr (BIAS) bv = ld_lane<W, P>(bias + v * P);
+      Lane<W, P> out;
 #pragma unroll
       for (int j = 0; j < P; ++j)
-        out.v[j] = fwd_elem<T, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv.v[j]), BIAS ? to_f32(bv.v[j]) : 0.f);
-      st16_stream(yr + v * P, out);
+        out.v[j] = fwd_elem<T, W, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv.v[j]), BIAS ? to_f32(bv.v[j]) : 0.f);
+      st_lane_stream(yr + v * P, out);
     }
   }
 }
@@ -139,10 +146,10 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_vec(const T* __restrict__ x, 
 // Persistent form of rmsnorm_fwd_vec for short launches: slot s of block b
 // takes rows b * RPB + s + k * stride, with w (and bias) in registers and the
 // next row's x in flight while the current row is reduced.
-template <typename T, int NTB, int TPR, int VPT, int MODE>
-__global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x, const T* __restrict__ w,
-                                                        const T* __restrict__ bias, const T* __restrict__ res,
-                                                        T* __restrict__ s_out, float offset, T* __restrict__ y,
+template <typename T, typename W, int NTB, int TPR, int VPT, int MODE>
+__global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x, const W* __restrict__ w,
+                                                        const W* __restrict__ bias, const T* __restrict__ res,
+                                                        T* __restrict__ s_out, float offset, W* __restrict__ y,
                                                         float* __restrict__ rstd, int64_t rows, int cols, float eps,
                                                         float inv_cols) {
   constexpr bool BIAS = MODE == kBias;
@@ -155,14 +162,14 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x,
   const int64_t first = (int64_t)blockIdx.x * RPB;
   const int64_t row0 = first + threadIdx.x / TPR;
   const int64_t trips = (rows - first + stride - 1) / stride;  // the same for every slot: barriers line up
-  Vec<T> wv[VPT], bv[VPT];
+  Lane<W, P> wv[VPT], bv[VPT];
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     const int v = lane + k * TPR;
     if (v < nvec) {
-      wv[k] = ld16(w + v * P);
+      wv[k] = ld_lane<W, P>(w + v * P);
       if constexpr (MODE == kAdd) wv[k] = offset_weight(wv[k], offset);
-      if constexpr (BIAS) bv[k] = ld16(bias + v * P);
+      if constexpr (BIAS) bv[k] = ld_lane<W, P>(bias + v * P);
     }
   }
   Vec<T> xv[VPT], xn[VPT];
@@ -205,11 +212,11 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x,
       for (int k = 0; k < VPT; ++k) {
         const int v = lane + k * TPR;
         if (v < nvec) {
-          Vec<T> out;
+          Lane<W, P> out;
 #pragma unroll
           for (int j = 0; j < P; ++j)
-            out.v[j] = fwd_elem<T, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv[k].v[j]), BIAS ? to_f32(bv[k].v[j]) : 0.f);
-          st16_stream(y + row * cols + v * P, out);
+            out.v[j] = fwd_elem<T, W, BIAS>(to_f32(xv[k].v[j]), r, to_f32(wv[k].v[j]), BIAS ? to_f32(bv[k].v[j]) : 0.f);
+          st_lane_stream(y + row * cols + v * P, out);
         }
       }
     }
@@ -222,10 +229,10 @@ __global__ __launch_bounds__(NTB) void rmsnorm_fwd_grid(const T* __restrict__ x,
 }
 
 // Any row width, any alignment: one block per row, two passes over x.
-template <typename T, int MODE>
-__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict__ x, const T* __restrict__ w,
-                                                            const T* __restrict__ bias, const T* __restrict__ res,
-                                                            T* __restrict__ s_out, float offset, T* __restrict__ y,
+template <typename T, typename W, int MODE>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict__ x, const W* __restrict__ w,
+                                                            const W* __restrict__ bias, const T* __restrict__ res,
+                                                            T* __restrict__ s_out, float offset, W* __restrict__ y,
                                                             float* __restrict__ rstd, int64_t rows, int cols,
                                                             float eps, float inv_cols) {
   constexpr bool BIAS = MODE == kBias;
@@ -245,11 +252,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_any(const T* __restrict_
   ss = row_sum<kThreads, kThreads>(ss, red);
   const float r = 1.0f / sqrtf(ss * inv_cols + eps);
   if (rstd != nullptr && threadIdx.x == 0) rstd[row] = r;
-  T* yr = y + row * cols;
+  W* yr = y + row * cols;
   const T* sr = MODE == kAdd ? s_out + row * cols : xr;
   for (int c = threadIdx.x; c < cols; c += kThreads) {
-    const float wv = MODE == kAdd ? to_f32(from_f32<T>(to_f32(w[c]) + offset)) : to_f32(w[c]);
-    yr[c] = fwd_elem<T, BIAS>(to_f32(sr[c]), r, wv, BIAS ? to_f32(bias[c]) : 0.f);
+    const float wv = MODE == kAdd ? to_f32(from_f32<W>(to_f32(w[c]) + offset)) : to_f32(w[c]);
+    yr[c] = fwd_elem<T, W, BIAS>(to_f32(sr[c]), r, wv, BIAS ? to_f32(bias[c]) : 0.f);
   }
 }
 
@@ -301,9 +308,9 @@ __device__ __forceinline__ void flush_partial(float (&acc)[VPT][P], float* lds_r
 
 // MODE kAdd: x is the residual sum s, w is used as w + offset, and ds (the
 // gradient reaching s from its second use, may be NULL) is added to dx.
-template <typename T, int NTB, int TPR, int VPT, int MODE>
-__global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, const T* __restrict__ w,
-                                                       const float* __restrict__ rstd, const T* __restrict__ dy,
+template <typename T, typename W, int NTB, int TPR, int VPT, int MODE>
+__global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, const W* __restrict__ w,
+                                                       const float* __restrict__ rstd, const W* __restrict__ dy,
                                                        const T* __restrict__ ds, float offset, T* __restrict__ dx,
                                                        float* __restrict__ dw_part, float* __restrict__ db_part,
                                                        int64_t rows, int cols, float inv_cols) {
@@ -322,8 +329,8 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     const int v = lane + k * TPR;
-    Vec<T> wv;
-    if (v < nvec) wv = ld16(w + v * P);
+    Lane<W, P> wv;
+    if (v < nvec) wv = ld_lane<W, P>(w + v * P);
     if constexpr (ADD) wv = offset_weight(wv, offset);
 #pragma unroll
     for (int j = 0; j < P; ++j) {
@@ -339,15 +346,16 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
   const int64_t row0 = (int64_t)blockIdx.x * RPB;
   const int64_t trips = (rows - row0 + stride - 1) / stride;
 
-  Vec<T> xv[VPT], gv[VPT], xn[VPT], gn[VPT];
+  Vec<T> xv[VPT], xn[VPT];
+  Lane<W, P> gv[VPT], gn[VPT];
   Vec<T> sv[ADD ? VPT : 1], sn[ADD ? VPT : 1];
-  auto fetch = [&](int64_t row, Vec<T>* xo, Vec<T>* go, Vec<T>* so) {
+  auto fetch = [&](int64_t row, Vec<T>* xo, Lane<W, P>* go, Vec<T>* so) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int v = lane + k * TPR;
       if (row < rows && v < nvec) {
         xo[k] = ld16_stream(x + row * cols + v * P);
-        go[k] = ld16_stream(dy + row * cols + v * P);
+        go[k] = ld_lane_stream<W, P>(dy + row * cols + v * P);
         if (has_ds) so[k] = ld16_stream(ds + row * cols + v * P);
       }
     }
@@ -406,10 +414,10 @@ __global__ __launch_bounds__(NTB) void rmsnorm_bwd_vec(const T* __restrict__ x, 
 
 // Any row width: block b walks rows b, b + G, ..., one column per thread per
 // step, one partial row per block.
-template <typename T, int MODE>
-__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict__ x, const T* __restrict__ w,
+template <typename T, typename W, int MODE>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict__ x, const W* __restrict__ w,
                                                             const float* __restrict__ rstd,
-                                                            const T* __restrict__ dy, const T* __restrict__ ds,
+                                                            const W* __restrict__ dy, const T* __restrict__ ds,
                                                             float offset, T* __restrict__ dx,
                                                             float* __restrict__ dw_part,
                                                             float* __restrict__ db_part, int64_t rows, int cols,
@@ -417,8 +425,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
   constexpr bool BIAS = MODE == kBias;
   constexpr bool ADD = MODE == kAdd;
   const bool has_ds = ADD && ds != nullptr;
-  // weight as the forward used it: w, or w + offset rounded to T
-  auto wc = [&](int c) { return ADD ? to_f32(from_f32<T>(to_f32(w[c]) + offset)) : to_f32(w[c]); };
+  // weight as the forward used it: w, or w + offset rounded to its type
+  auto wc = [&](int c) { return ADD ? to_f32(from_f32<W>(to_f32(w[c]) + offset)) : to_f32(w[c]); };
   __shared__ float red[kThreads / 64];
   float* dwp = dw_part + (int64_t)blockIdx.x * cols;
   float* dbp = BIAS ? db_part + (int64_t)blockIdx.x * cols : nullptr;
@@ -429,7 +437,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_any(const T* __restrict_
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const float r = rstd[row];
     const T* xr = x + row * cols;
-    const T* gr = dy + row * cols;
+    const W* gr = dy + row * cols;
     float dot = 0.f;
     for (int c = threadIdx.x; c < cols; c += kThreads) dot += to_f32(gr[c]) * wc(c) * (to_f32(xr[c]) * r);
     dot = row_sum<kThreads, kThreads>(dot, red) * inv_cols;
@@ -500,15 +508,15 @@ template <typename K> int resident_per_cu(K kernel, int threads, size_t lds) {
   return n;
 }
 
-template <typename T, int MODE, int NTB, int TPR, int VPT> int bwd_resident() {
+template <typename T, typename W, int MODE, int NTB, int TPR, int VPT> int bwd_resident() {
   // dynamic LDS of a 4-rows-per-block shape: one fp32 row of at most 64*4*8 columns
-  static const int n = resident_per_cu(rmsnorm_bwd_vec<T, NTB, TPR, VPT, MODE>, NTB,
+  static const int n = resident_per_cu(rmsnorm_bwd_vec<T, W, NTB, TPR, VPT, MODE>, NTB,
                                        NTB / TPR > 1 ? (size_t)64 * 4 * 8 * sizeof(float) : 0);
   return n;
 }
 
-template <typename T, int MODE> int bwd_any_resident() {
-  static const int n = resident_per_cu(rmsnorm_bwd_any<T, MODE>, kThreads, 0);
+template <typename T, typename W, int MODE> int bwd_any_resident() {
+  static const int n = resident_per_cu(rmsnorm_bwd_any<T, W, MODE>, kThreads, 0);
   return n;
 }
 
@@ -524,23 +532,24 @@ struct FwdArgs {
   hipStream_t s;
 };
 
-template <typename T, int MODE, int NTB, int TPR, int VPT> void launch_fwd_vec(const FwdArgs& a) {
+template <typename T, typename W, int MODE, int NTB, int TPR, int VPT> void launch_fwd_vec(const FwdArgs& a) {
   constexpr int RPB = NTB / TPR;
   const int64_t groups = (a.rows + RPB - 1) / RPB;
-  const T *x = static_cast<const T*>(a.x), *w = static_cast<const T*>(a.w), *b = static_cast<const T*>(a.b),
-          *res = static_cast<const T*>(a.res);
-  T *s_out = static_cast<T*>(a.s_out), *y = static_cast<T*>(a.y);
+  const T *x = static_cast<const T*>(a.x), *res = static_cast<const T*>(a.res);
+  const W *w = static_cast<const W*>(a.w), *b = static_cast<const W*>(a.b);
+  T* s_out = static_cast<T*>(a.s_out);
+  W* y = static_cast<W*>(a.y);
   // Up to four waves of resident blocks: the persistent grid.
-  static const int per_cu = resident_per_cu(rmsnorm_fwd_vec<T, NTB, TPR, VPT, MODE>, NTB, 0);
-  static const int per_cu_grid = resident_per_cu(rmsnorm_fwd_grid<T, NTB, TPR, VPT, MODE>, NTB, 0);
+  static const int per_cu = resident_per_cu(rmsnorm_fwd_vec<T, W, NTB, TPR, VPT, MODE>, NTB, 0);
+  static const int per_cu_grid = resident_per_cu(rmsnorm_fwd_grid<T, W, NTB, TPR, VPT, MODE>, NTB, 0);
   if (groups <= (int64_t)4 * cu_count() * per_cu) {
     const int64_t slots = (int64_t)cu_count() * per_cu_grid;
-    hipLaunchKernelGGL((rmsnorm_fwd_grid<T, NTB, TPR, VPT, MODE>), dim3(groups < slots ? groups : slots), dim3(NTB), 0,
-                       a.s, x, w, b, res, s_out, a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
+    hipLaunchKernelGGL((rmsnorm_fwd_grid<T, W, NTB, TPR, VPT, MODE>), dim3(groups < slots ? groups : slots), dim3(NTB),
+                       0, a.s, x, w, b, res, s_out, a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
     return;
   }
-  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, NTB, TPR, VPT, MODE>), dim3(groups), dim3(NTB), 0, a.s, x, w, b, res, s_out,
-                     a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
+  hipLaunchKernelGGL((rmsnorm_fwd_vec<T, W, NTB, TPR, VPT, MODE>), dim3(groups), dim3(NTB), 0, a.s, x, w, b, res,
+                     s_out, a.offset, y, a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
 }
 
 struct BwdArgs {
@@ -554,11 +563,12 @@ struct BwdArgs {
   hipStream_t s;
 };
 
-template <typename T, int MODE, int NTB, int TPR, int VPT> void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
+template <typename T, typename W, int MODE, int NTB, int TPR, int VPT>
+void launch_bwd_vec(const BwdArgs& a, int64_t blocks) {
   constexpr int RPB = NTB / TPR;
   const size_t lds = RPB > 1 ? (size_t)a.cols * sizeof(float) : 0;
-  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, NTB, TPR, VPT, MODE>), dim3(blocks), dim3(NTB), lds, a.s,
-                     static_cast<const T*>(a.x), static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy),
+  hipLaunchKernelGGL((rmsnorm_bwd_vec<T, W, NTB, TPR, VPT, MODE>), dim3(blocks), dim3(NTB), lds, a.s,
+                     static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.rstd, static_cast<const W*>(a.dy),
                      static_cast<const T*>(a.ds), a.offset, static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows,
                      a.cols, 1.0f / (float)a.cols);
 }
@@ -569,63 +579,64 @@ template <typename T, int MODE, int NTB, int TPR, int VPT> void launch_bwd_vec(c
 #define PK_RMS_BWD_SHAPES(X) X(256, 64, 1) X(256, 64, 2) X(256, 64, 4) X(256, 256, 2) X(512, 512, 2) \
   X(1024, 1024, 2) X(1024, 1024, 4) X(1024, 1024, 8) X(1024, 1024, 16)
 
-template <typename T, int MODE> int fwd(const FwdArgs& a, const char* who) {
+template <typename T, typename W, int MODE> int fwd(const FwdArgs& a, const char* who) {
   const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.y) && (MODE != kBias || aligned16(a.b)) &&
                        (MODE != kAdd || (aligned16(a.res) && aligned16(a.s_out)));
   const Plan p = plan_for(a.cols, sizeof(T), aligned, false);
   bool done = false;
 #define PK_FWD_CASE(NTB, TPR, VPT)                                                         \
   if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
-    launch_fwd_vec<T, MODE, NTB, TPR, VPT>(a);                                            \
+    launch_fwd_vec<T, W, MODE, NTB, TPR, VPT>(a);                                         \
     done = true;                                                                           \
   }
   PK_RMS_FWD_SHAPES(PK_FWD_CASE)
 #undef PK_FWD_CASE
   if (!done)
-    hipLaunchKernelGGL((rmsnorm_fwd_any<T, MODE>), dim3(a.rows), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
-                       static_cast<const T*>(a.w), static_cast<const T*>(a.b), static_cast<const T*>(a.res),
-                       static_cast<T*>(a.s_out), a.offset, static_cast<T*>(a.y), a.rstd, a.rows, a.cols, a.eps,
-                       1.0f / (float)a.cols);
+    hipLaunchKernelGGL((rmsnorm_fwd_any<T, W, MODE>), dim3(a.rows), dim3(kThreads), 0, a.s,
+                       static_cast<const T*>(a.x), static_cast<const W*>(a.w), static_cast<const W*>(a.b),
+                       static_cast<const T*>(a.res), static_cast<T*>(a.s_out), a.offset, static_cast<W*>(a.y),
+                       a.rstd, a.rows, a.cols, a.eps, 1.0f / (float)a.cols);
   return launched(who);
 }
 
 // Persistent backward grid: every resident block slot of the device, never
 // more blocks than the rows need.
-template <typename T, int MODE> int64_t bwd_blocks(int64_t rows, const Plan& p) {
+template <typename T, typename W, int MODE> int64_t bwd_blocks(int64_t rows, const Plan& p) {
   int per_cu = 0;
   int64_t rpb = 1;
 #define PK_RES_CASE(NTB, TPR, VPT)                                                         \
   if (!per_cu && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                 \
-    per_cu = bwd_resident<T, MODE, NTB, TPR, VPT>();                                      \
+    per_cu = bwd_resident<T, W, MODE, NTB, TPR, VPT>();                                   \
     rpb = NTB / TPR;                                                                       \
   }
   PK_RMS_BWD_SHAPES(PK_RES_CASE)
 #undef PK_RES_CASE
-  if (!per_cu) per_cu = bwd_any_resident<T, MODE>();
+  if (!per_cu) per_cu = bwd_any_resident<T, W, MODE>();
   const int64_t want = (rows + rpb - 1) / rpb;
   const int64_t cap = (int64_t)cu_count() * per_cu;
   return want < cap ? want : cap;
 }
 
-template <typename T, int MODE> int bwd(const BwdArgs& a, const char* who) {
+template <typename T, typename W, int MODE> int bwd(const BwdArgs& a, const char* who) {
   const bool aligned = aligned16(a.x) && aligned16(a.w) && aligned16(a.dy) && aligned16(a.dx) &&
                        (a.ds == nullptr || aligned16(a.ds));
   const Plan p = plan_for(a.cols, sizeof(T), aligned, true);
-  const int64_t blocks = bwd_blocks<T, MODE>(a.rows, p);
+  const int64_t blocks = bwd_blocks<T, W, MODE>(a.rows, p);
   bool done = false;
 #define PK_BWD_CASE(NTB, TPR, VPT)                                                         \
   if (!done && p.vec && p.ntb == NTB && p.tpr == TPR && p.vpt == VPT) {                   \
-    launch_bwd_vec<T, MODE, NTB, TPR, VPT>(a, blocks);                                    \
+    launch_bwd_vec<T, W, MODE, NTB, TPR, VPT>(a, blocks);                                 \
     done = true;                                                                           \
   }
   PK_RMS_BWD_SHAPES(PK_BWD_CASE)
 #undef PK_BWD_CASE
   if (!done)
-    hipLaunchKernelGGL((rmsnorm_bwd_any<T, MODE>), dim3(blocks), dim3(kThreads), 0, a.s, static_cast<const T*>(a.x),
-                       static_cast<const T*>(a.w), a.rstd, static_cast<const T*>(a.dy), static_cast<const T*>(a.ds),
-                       a.offset, static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows, a.cols, 1.0f / (float)a.cols);
-  column_sums<T>(a.dw_part, a.stage, static_cast<T*>(a.dw), blocks, a.cols, a.s);
-  if (MODE == kBias) column_sums<T>(a.db_part, a.stage, static_cast<T*>(a.db), blocks, a.cols, a.s);
+    hipLaunchKernelGGL((rmsnorm_bwd_any<T, W, MODE>), dim3(blocks), dim3(kThreads), 0, a.s,
+                       static_cast<const T*>(a.x), static_cast<const W*>(a.w), a.rstd, static_cast<const W*>(a.dy),
+                       static_cast<const T*>(a.ds), a.offset, static_cast<T*>(a.dx), a.dw_part, a.db_part, a.rows,
+                       a.cols, 1.0f / (float)a.cols);
+  column_sums<W>(a.dw_part, a.stage, static_cast<W*>(a.dw), blocks, a.cols, a.s);
+  if (MODE == kBias) column_sums<W>(a.db_part, a.stage, static_cast<W*>(a.db), blocks, a.cols, a.s);
   return launched(who);
 }
 
@@ -635,10 +646,10 @@ struct Layout {
   int64_t part, stage, total;
 };
 
-template <typename T, int MODE> Layout layout_for(int64_t rows, int64_t cols) {
+template <typename T, typename W, int MODE> Layout layout_for(int64_t rows, int64_t cols) {
   // The aligned plan and the fallback may use different grids: size for the larger.
-  const int64_t b1 = bwd_blocks<T, MODE>(rows, plan_for(cols, sizeof(T), true, true));
-  const int64_t b2 = bwd_blocks<T, MODE>(rows, plan_for(cols, sizeof(T), false, true));
+  const int64_t b1 = bwd_blocks<T, W, MODE>(rows, plan_for(cols, sizeof(T), true, true));
+  const int64_t b2 = bwd_blocks<T, W, MODE>(rows, plan_for(cols, sizeof(T), false, true));
   const int64_t blocks = b1 > b2 ? b1 : b2;
   auto up = [](int64_t n) { return (n + 255) / 256 * 256; };
   Layout l;
@@ -648,49 +659,70 @@ template <typename T, int MODE> Layout layout_for(int64_t rows, int64_t cols) {
   return l;
 }
 
-template <int MODE> Layout layout_of(int64_t rows, int64_t cols, int dtype) {
+// (x dtype, weight dtype) pairs the kernels implement: one dtype, or a 16-bit x
+// with an fp32 weight (not in the residual-add mode, whose reference adds at
+// one dtype).
+bool supported_pair(int dtype, int wdtype, int mode) {
+  if (wdtype == dtype) return known_dtype(dtype);
+  return mode != kAdd && wdtype == PK_F32 && (dtype == PK_BF16 || dtype == PK_F16);
+}
+
+template <int MODE> Layout layout_of(int64_t rows, int64_t cols, int dtype, int wdtype) {
+  if constexpr (MODE != kAdd) {
+    if (wdtype != dtype) return dtype == PK_BF16 ? layout_for<bf16, float, MODE>(rows, cols)
+                                                 : layout_for<f16, float, MODE>(rows, cols);
+  }
   switch (dtype) {
-    case PK_F32: return layout_for<float, MODE>(rows, cols);
-    case PK_BF16: return layout_for<bf16, MODE>(rows, cols);
-    default: return layout_for<f16, MODE>(rows, cols);
+    case PK_F32: return layout_for<float, float, MODE>(rows, cols);
+    case PK_BF16: return layout_for<bf16, bf16, MODE>(rows, cols);
+    default: return layout_for<f16, f16, MODE>(rows, cols);
   }
 }
 
-Layout workspace_layout(int64_t rows, int64_t cols, int dtype, int mode) {
-  return mode == kBias ? layout_of<kBias>(rows, cols, dtype)
-                       : mode == kAdd ? layout_of<kAdd>(rows, cols, dtype) : layout_of<kPlain>(rows, cols, dtype);
+Layout workspace_layout(int64_t rows, int64_t cols, int dtype, int wdtype, int mode) {
+  return mode == kBias ? layout_of<kBias>(rows, cols, dtype, wdtype)
+                       : mode == kAdd ? layout_of<kAdd>(rows, cols, dtype, wdtype)
+                                      : layout_of<kPlain>(rows, cols, dtype, wdtype);
 }
 
-// One workspace size serves every backward entry point and mode.
+// One workspace size serves every backward entry point, mode and weight dtype.
 int64_t workspace_bytes(int64_t rows, int64_t cols, int dtype) {
   int64_t n = 0;
-  for (int mode : {kPlain, kBias, kAdd}) {
-    const int64_t t = workspace_layout(rows, cols, dtype, mode).total;
-    n = t > n ? t : n;
-  }
+  for (int wdtype : {dtype, (int)PK_F32})
+    for (int mode : {kPlain, kBias, kAdd}) {
+      if (!supported_pair(dtype, wdtype, mode)) continue;
+      const int64_t t = workspace_layout(rows, cols, dtype, wdtype, mode).total;
+      n = t > n ? t : n;
+    }
   return n;
 }
 
-template <int MODE> int fwd_dispatch(const FwdArgs& a, int dtype, const char* who) {
+template <int MODE> int fwd_dispatch(const FwdArgs& a, int dtype, int wdtype, const char* who) {
+  if constexpr (MODE != kAdd) {
+    if (wdtype != dtype) return dtype == PK_BF16 ? fwd<bf16, float, MODE>(a, who) : fwd<f16, float, MODE>(a, who);
+  }
   switch (dtype) {
-    case PK_F32: return fwd<float, MODE>(a, who);
-    case PK_BF16: return fwd<bf16, MODE>(a, who);
-    default: return fwd<f16, MODE>(a, who);
+    case PK_F32: return fwd<float, float, MODE>(a, who);
+    case PK_BF16: return fwd<bf16, bf16, MODE>(a, who);
+    default: return fwd<f16, f16, MODE>(a, who);
   }
 }
 
-template <int MODE> int bwd_dispatch(const BwdArgs& a, int dtype, const char* who) {
+template <int MODE> int bwd_dispatch(const BwdArgs& a, int dtype, int wdtype, const char* who) {
+  if constexpr (MODE != kAdd) {
+    if (wdtype != dtype) return dtype == PK_BF16 ? bwd<bf16, float, MODE>(a, who) : bwd<f16, float, MODE>(a, who);
+  }
   switch (dtype) {
-    case PK_F32: return bwd<float, MODE>(a, who);
-    case PK_BF16: return bwd<bf16, MODE>(a, who);
-    default: return bwd<f16, MODE>(a, who);
+    case PK_F32: return bwd<float, float, MODE>(a, who);
+    case PK_BF16: return bwd<bf16, bf16, MODE>(a, who);
+    default: return bwd<f16, f16, MODE>(a, who);
   }
 }
 
 // Splits the caller's workspace for a backward call of this mode.
-int carve(const char* who, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, int mode,
-          BwdArgs& a) {
-  const Layout l = workspace_layout(rows, cols, dtype, mode);
+int carve(const char* who, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype,
+          int wdtype, int mode, BwdArgs& a) {
+  const Layout l = workspace_layout(rows, cols, dtype, wdtype, mode);
   if (workspace_bytes < l.total)
     return fail(PK_ERR_INVALID, "%s: workspace of %lld bytes, need %lld", who, (long long)workspace_bytes,
                 (long long)l.total);
@@ -702,11 +734,14 @@ int carve(const char* who, void* workspace, int64_t workspace_bytes, int64_t row
   return PK_OK;
 }
 
-int check_shape(const char* who, int64_t rows, int64_t cols, int dtype) {
+int check_shape(const char* who, int64_t rows, int64_t cols, int dtype, int wdtype = -1, int mode = kPlain) {
   if (rows < 0 || cols < 0) return fail(PK_ERR_INVALID, "%s: negative shape (%lld, %lld)", who, (long long)rows,
                                         (long long)cols);
   if (cols > (int64_t)1 << 30) return fail(PK_ERR_UNSUPPORTED, "%s: %lld columns", who, (long long)cols);
   if (!known_dtype(dtype)) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d", who, dtype);
+  if (!supported_pair(dtype, wdtype < 0 ? dtype : wdtype, mode))
+    return fail(PK_ERR_UNSUPPORTED, "%s: x dtype code %d with weight dtype code %d (one dtype, or a 16-bit x with an "
+                "fp32 weight)", who, dtype, wdtype);
   return PK_OK;
 }
 
@@ -757,15 +792,15 @@ int scratch_address(const char* who, void** out) {
 extern "C" {
 
 int pk_rmsnorm_fwd(const void* x, const void* w, const void* bias, void* y, float* rstd, int64_t rows, int64_t cols,
-                   float eps, int dtype, void* stream) {
+                   float eps, int dtype, int w_dtype, void* stream) {
   using namespace pk;
-  if (int st = check_shape("pk_rmsnorm_fwd", rows, cols, dtype)) return st;
+  if (int st = check_shape("pk_rmsnorm_fwd", rows, cols, dtype, w_dtype)) return st;
   if (rows == 0) return PK_OK;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_rmsnorm_fwd: zero-width rows");
   if (!x || !w || !y) return fail(PK_ERR_INVALID, "pk_rmsnorm_fwd: null pointer");
   const FwdArgs a{x, w, bias, nullptr, nullptr, 0.f, y, rstd, rows, (int)cols, eps, static_cast<hipStream_t>(stream)};
-  return bias != nullptr ? fwd_dispatch<kBias>(a, dtype, "pk_rmsnorm_fwd")
-                         : fwd_dispatch<kPlain>(a, dtype, "pk_rmsnorm_fwd");
+  return bias != nullptr ? fwd_dispatch<kBias>(a, dtype, w_dtype, "pk_rmsnorm_fwd")
+                         : fwd_dispatch<kPlain>(a, dtype, w_dtype, "pk_rmsnorm_fwd");
 }
 
 int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype) {
@@ -775,10 +810,11 @@ int64_t pk_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype) {
 }
 
 int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw, void* dbias,
-                   void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, void* stream) {
+                   void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, int dtype, int w_dtype,
+                   void* stream) {
   using namespace pk;
   const char* who = "pk_rmsnorm_bwd";
-  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (int st = check_shape(who, rows, cols, dtype, w_dtype)) return st;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: zero-width rows");
   if (!x || !w || !rstd || !dy || !dx || !dw || !workspace)
     return fail(PK_ERR_INVALID, "pk_rmsnorm_bwd: null pointer");
@@ -786,20 +822,20 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
   const int mode = dbias != nullptr ? kBias : kPlain;
   BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
-  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, mode, a)) return st;
-  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, who) : bwd_dispatch<kPlain>(a, dtype, who);
+  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, w_dtype, mode, a)) return st;
+  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, w_dtype, who) : bwd_dispatch<kPlain>(a, dtype, w_dtype, who);
 }
 
 int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, const void* dy, void* dx, void* dw,
-                           void* dbias, int64_t rows, int64_t cols, int dtype, void* stream) {
+                           void* dbias, int64_t rows, int64_t cols, int dtype, int w_dtype, void* stream) {
   using namespace pk;
   const char* who = "pk_rmsnorm_bwd_noalloc";
-  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (int st = check_shape(who, rows, cols, dtype, w_dtype)) return st;
   if (cols == 0) return fail(PK_ERR_INVALID, "%s: zero-width rows", who);
   if (!x || !w || !rstd || !dy || !dx || !dw) return fail(PK_ERR_INVALID, "%s: null pointer", who);
   if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "%s: zero rows (dw is all zeros; fill it host-side)", who);
   const int mode = dbias != nullptr ? kBias : kPlain;
-  const int64_t need = workspace_layout(rows, cols, dtype, mode).total;
+  const int64_t need = workspace_layout(rows, cols, dtype, w_dtype, mode).total;
   if (need > kScratchBytes)
     return fail(PK_ERR_UNSUPPORTED, "%s: shape (%lld, %lld) needs %lld bytes of scratch, the fixed array holds %lld",
                 who, (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
@@ -807,8 +843,8 @@ int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, cons
   if (int st = scratch_address(who, &base)) return st;
   BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
-  if (int st = carve(who, base, kScratchBytes, rows, cols, dtype, mode, a)) return st;
-  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, who) : bwd_dispatch<kPlain>(a, dtype, who);
+  if (int st = carve(who, base, kScratchBytes, rows, cols, dtype, w_dtype, mode, a)) return st;
+  return mode == kBias ? bwd_dispatch<kBias>(a, dtype, w_dtype, who) : bwd_dispatch<kPlain>(a, dtype, w_dtype, who);
 }
 
 int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y, void* s, float* rstd,
@@ -821,7 +857,7 @@ int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void*
   if (!x || !residual || !w || !y || !s) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: null pointer");
   if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: offset is not finite");
   const FwdArgs a{x, w, nullptr, residual, s, offset, y, rstd, rows, (int)cols, eps, static_cast<hipStream_t>(stream)};
-  return fwd_dispatch<kAdd>(a, dtype, who);
+  return fwd_dispatch<kAdd>(a, dtype, dtype, who);
 }
 
 int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const void* dy, const void* ds, void* dx,
@@ -837,8 +873,8 @@ int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const vo
   if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: offset is not finite");
   BwdArgs a{s, w, dy, ds, offset, rstd, dx, dw, nullptr, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
-  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, kAdd, a)) return st;
-  return bwd_dispatch<kAdd>(a, dtype, who);
+  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, dtype, kAdd, a)) return st;
+  return bwd_dispatch<kAdd>(a, dtype, dtype, who);
 }
 
 }  // extern "C"

@@ -9,6 +9,9 @@
 // transpose (the backward) is dx[j] = dy[j] cos[j] + dy[j + h] sin[j + h],
 // dx[j + h] = dy[j + h] cos[j + h] - dy[j] sin[j]. The two halves of a table
 // row need not be equal. Arithmetic is fp32 with one rounding per output.
+// Inputs and outputs may differ in type: 16-bit q/k with fp32 tables give fp32
+// outputs (torch's promotion), whose backward reads fp32 cotangents and writes
+// 16-bit gradients.
 //
 // A block takes a tile of positions of one batch row and a group of heads
 // (q heads first, then k heads); a thread owns one (position, chunk) of the
@@ -39,19 +42,26 @@ struct RopeArgs {
   int group;   // heads per block (of q_heads + kv_heads)
 };
 
-template <typename T, int VEC> struct Pack {
+// VEC elements of T: whole 16-byte non-temporal accesses when they fill them
+// (one or two, when a wider type lines up with a 16-bit one), else elements.
+template <typename T, int VEC> struct alignas(16) Pack {
+  static constexpr bool kWhole = VEC * sizeof(T) % 16 == 0;
   T v[VEC];
   __device__ __forceinline__ void load(const T* p) {
-    if constexpr (VEC * sizeof(T) == 16) {
-      *reinterpret_cast<u32x4*>(v) = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    if constexpr (kWhole) {
+#pragma unroll
+      for (int i = 0; i < (int)(VEC * sizeof(T) / 16); ++i)
+        reinterpret_cast<u32x4*>(v)[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + i);
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[j] = p[j];
     }
   }
   __device__ __forceinline__ void store(T* p) const {
-    if constexpr (VEC * sizeof(T) == 16) {
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(v), reinterpret_cast<u32x4*>(p));
+    if constexpr (kWhole) {
+#pragma unroll
+      for (int i = 0; i < (int)(VEC * sizeof(T) / 16); ++i)
+        __builtin_nontemporal_store(reinterpret_cast<const u32x4*>(v)[i], reinterpret_cast<u32x4*>(p) + i);
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) p[j] = v[j];
@@ -76,7 +86,7 @@ template <typename C, int N> __device__ __forceinline__ void table(const C* p, f
   }
 }
 
-template <typename T, typename C, int VEC, int U, bool TRANSPOSE>
+template <typename TI, typename TO, typename C, int VEC, int U, bool TRANSPOSE>
 __global__ __launch_bounds__(kThreads) void rope_kernel(const C* __restrict__ cosp, const C* __restrict__ sinp,
                                                         RopeArgs a) {
   // block -> (head group, batch, tile); consecutive blocks take consecutive tiles
@@ -105,14 +115,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const C* __restrict__ co
     const int64_t xo[2] = {b * a.xs[0][0] + s * a.xs[0][2] + j, b * a.xs[1][0] + s * a.xs[1][2] + j};
     const int64_t yo[2] = {b * a.ys[0][0] + s * a.ys[0][2] + j, b * a.ys[1][0] + s * a.ys[1][2] + j};
     for (int hh = h_begin; hh < h_end; hh += U) {
-      Pack<T, VEC> x1[U], x2[U];
+      Pack<TI, VEC> x1[U], x2[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int g = hh + u;
         if (g >= h_end) break;
         const int t = g >= a.heads[0];
         const int h = t ? g - a.heads[0] : g;
-        const T* xr = static_cast<const T*>(a.x[t]) + xo[t] + h * a.xs[t][1];
+        const TI* xr = static_cast<const TI*>(a.x[t]) + xo[t] + h * a.xs[t][1];
         x1[u].load(xr);
         x2[u].load(xr + a.half);
       }
@@ -122,19 +132,19 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const C* __restrict__ co
         if (g >= h_end) break;
         const int t = g >= a.heads[0];
         const int h = t ? g - a.heads[0] : g;
-        Pack<T, VEC> y1, y2;
+        Pack<TO, VEC> y1, y2;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
           const float p = to_f32(x1[u].v[k]), q = to_f32(x2[u].v[k]);
           if constexpr (!TRANSPOSE) {
-            y1.v[k] = from_f32<T>(p * c1[k] - q * s1[k]);
-            y2.v[k] = from_f32<T>(q * c2[k] + p * s2[k]);
+            y1.v[k] = from_f32<TO>(p * c1[k] - q * s1[k]);
+            y2.v[k] = from_f32<TO>(q * c2[k] + p * s2[k]);
           } else {
-            y1.v[k] = from_f32<T>(p * c1[k] + q * s2[k]);
-            y2.v[k] = from_f32<T>(q * c2[k] - p * s1[k]);
+            y1.v[k] = from_f32<TO>(p * c1[k] + q * s2[k]);
+            y2.v[k] = from_f32<TO>(q * c2[k] - p * s1[k]);
           }
         }
-        T* yr = static_cast<T*>(a.y[t]) + yo[t] + h * a.ys[t][1];
+        TO* yr = static_cast<TO*>(a.y[t]) + yo[t] + h * a.ys[t][1];
         y1.store(yr);
         y2.store(yr + a.half);
       }
@@ -142,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const C* __restrict__ co
   }
 }
 
-template <typename T, typename C, int VEC>
+template <typename TI, typename TO, typename C, int VEC>
 int launch(const void* cs, const void* sn, RopeArgs a, int transpose, hipStream_t s) {
   constexpr int U = 4;
   a.chunks = a.half / VEC;
@@ -161,27 +171,51 @@ int launch(const void* cs, const void* sn, RopeArgs a, int transpose, hipStream_
   if (blocks == 0) return PK_OK;
   if (blocks > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "pk_rope: %lld blocks exceed the grid", (long long)blocks);
   if (transpose)
-    hipLaunchKernelGGL((rope_kernel<T, C, VEC, U, true>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL((rope_kernel<TI, TO, C, VEC, U, true>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
                        static_cast<const C*>(cs), static_cast<const C*>(sn), a);
   else
-    hipLaunchKernelGGL((rope_kernel<T, C, VEC, U, false>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL((rope_kernel<TI, TO, C, VEC, U, false>), dim3((unsigned)blocks), dim3(kThreads), 0, s,
                        static_cast<const C*>(cs), static_cast<const C*>(sn), a);
   return launched("pk_rope");
 }
 
-template <typename T, typename C> int run(bool vec, const void* cs, const void* sn, const RopeArgs& a, int tr,
-                                          hipStream_t s) {
-  constexpr int V = 16 / sizeof(T);
-  return vec ? launch<T, C, V>(cs, sn, a, tr, s) : launch<T, C, 1>(cs, sn, a, tr, s);
+// Chunks are 16 bytes of the narrower of the input and output types.
+template <typename TI, typename TO> constexpr int kRopeVec = 16 / (sizeof(TI) < sizeof(TO) ? sizeof(TI) : sizeof(TO));
+
+template <typename TI, typename TO, typename C>
+int run(bool vec, const void* cs, const void* sn, const RopeArgs& a, int tr, hipStream_t s) {
+  return vec ? launch<TI, TO, C, kRopeVec<TI, TO>>(cs, sn, a, tr, s) : launch<TI, TO, C, 1>(cs, sn, a, tr, s);
 }
 
-template <typename T> int run_cs(int cs_dtype, bool vec, const void* cs, const void* sn, const RopeArgs& a, int tr,
-                                 hipStream_t s) {
+template <typename TI, typename TO>
+int run_cs(int cs_dtype, bool vec, const void* cs, const void* sn, const RopeArgs& a, int tr, hipStream_t s) {
   switch (cs_dtype) {
-    case PK_F32: return run<T, float>(vec, cs, sn, a, tr, s);
-    case PK_BF16: return run<T, bf16>(vec, cs, sn, a, tr, s);
-    default: return run<T, f16>(vec, cs, sn, a, tr, s);
+    case PK_F32: return run<TI, TO, float>(vec, cs, sn, a, tr, s);
+    case PK_BF16: return run<TI, TO, bf16>(vec, cs, sn, a, tr, s);
+    default: return run<TI, TO, f16>(vec, cs, sn, a, tr, s);
   }
+}
+
+// Input/output type pairs: one type, or a 16-bit type with fp32 either way.
+bool rope_pair(int in_dtype, int out_dtype) {
+  if (!known_dtype(in_dtype) || !known_dtype(out_dtype)) return false;
+  return in_dtype == out_dtype || in_dtype == PK_F32 || out_dtype == PK_F32;
+}
+
+int run_types(int in_dtype, int out_dtype, int cs_dtype, bool vec, const void* cs, const void* sn, const RopeArgs& a,
+              int tr, hipStream_t s) {
+  if (in_dtype == out_dtype) {
+    switch (in_dtype) {
+      case PK_F32: return run_cs<float, float>(cs_dtype, vec, cs, sn, a, tr, s);
+      case PK_BF16: return run_cs<bf16, bf16>(cs_dtype, vec, cs, sn, a, tr, s);
+      default: return run_cs<f16, f16>(cs_dtype, vec, cs, sn, a, tr, s);
+    }
+  }
+  if (out_dtype == PK_F32)
+    return in_dtype == PK_BF16 ? run_cs<bf16, float>(cs_dtype, vec, cs, sn, a, tr, s)
+                               : run_cs<f16, float>(cs_dtype, vec, cs, sn, a, tr, s);
+  return out_dtype == PK_BF16 ? run_cs<float, bf16>(cs_dtype, vec, cs, sn, a, tr, s)
+                              : run_cs<float, f16>(cs_dtype, vec, cs, sn, a, tr, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -269,7 +303,8 @@ __device__ __forceinline__ NormBlock norm_block(const NormArgs& a) {
   return nb;
 }
 
-template <typename T, typename C, int VEC, int U>
+// T: q, k and the weights; TO: the outputs (T, or fp32 beside fp32 tables)
+template <typename T, typename TO, typename C, int VEC, int U>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __restrict__ cosp,
                                                                     const C* __restrict__ sinp, NormArgs a) {
   const NormBlock nb = norm_block(a);
@@ -286,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __r
   table(wp + j, w1);
   table(wp + a.half + j, w2);
   const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
-  T* yb = static_cast<T*>(a.y[t]) + nb.b * a.ys[t][0] + nb.s * a.ys[t][2] + j;
+  TO* yb = static_cast<TO*>(a.y[t]) + nb.b * a.ys[t][0] + nb.s * a.ys[t][2] + j;
   float* rb = a.rstd[t] + ((int64_t)nb.b * a.heads[t]) * a.seq + nb.s;
   for (int h0 = nb.h_begin; h0 < nb.h_end; h0 += U) {
     Pack<T, VEC> x1[U], x2[U];
@@ -307,14 +342,14 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __r
         ss += p * p + q * q;
       }
       const float r = rsqrtf(row_sum(ss, a.chunks) * a.inv_d + a.eps);
-      Pack<T, VEC> y1, y2;
+      Pack<TO, VEC> y1, y2;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         const float n1 = to_f32(x1[u].v[k]) * r * w1[k], n2 = to_f32(x2[u].v[k]) * r * w2[k];
-        y1.v[k] = from_f32<T>(n1 * c1[k] - n2 * s1[k]);
-        y2.v[k] = from_f32<T>(n2 * c2[k] + n1 * s2[k]);
+        y1.v[k] = from_f32<TO>(n1 * c1[k] - n2 * s1[k]);
+        y2.v[k] = from_f32<TO>(n2 * c2[k] + n1 * s2[k]);
       }
-      T* yr = yb + (h0 + u) * a.ys[t][1];
+      TO* yr = yb + (h0 + u) * a.ys[t][1];
       y1.store(yr);
       y2.store(yr + a.half);
       if (nb.j == 0) rb[(int64_t)(h0 + u) * a.seq] = r;
@@ -322,7 +357,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __r
   }
 }
 
-template <typename T, typename C, int VEC, int U>
+// T: q, k, the weights and their gradients; TG: the cotangents (the forward's output type)
+template <typename T, typename TG, typename C, int VEC, int U>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_bwd_kernel(const C* __restrict__ cosp,
                                                                     const C* __restrict__ sinp, NormArgs a) {
   extern __shared__ float red[];  // [4 waves][2 * half]
@@ -343,17 +379,18 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_bwd_kernel(const C* __r
     table(wp + j, w1);
     table(wp + a.half + j, w2);
     const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
-    const T* gb = static_cast<const T*>(a.g[t]) + nb.b * a.gs[t][0] + nb.s * a.gs[t][2] + j;
+    const TG* gb = static_cast<const TG*>(a.g[t]) + nb.b * a.gs[t][0] + nb.s * a.gs[t][2] + j;
     T* db = static_cast<T*>(a.y[t]) + nb.b * a.ys[t][0] + nb.s * a.ys[t][2] + j;
     const float* rb = a.rstd[t] + ((int64_t)nb.b * a.heads[t]) * a.seq + nb.s;
     for (int h0 = nb.h_begin; h0 < nb.h_end; h0 += U) {
-      Pack<T, VEC> x1[U], x2[U], g1[U], g2[U];
+      Pack<T, VEC> x1[U], x2[U];
+      Pack<TG, VEC> g1[U], g2[U];
       float r[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (h0 + u >= nb.h_end) break;
         const T* xr = xb + (h0 + u) * a.xs[t][1];
-        const T* gr = gb + (h0 + u) * a.gs[t][1];
+        const TG* gr = gb + (h0 + u) * a.gs[t][1];
         x1[u].load(xr);
         x2[u].load(xr + a.half);
         g1[u].load(gr);
@@ -433,7 +470,8 @@ int64_t norm_workspace(const NormPlan& p, int64_t head_dim) {
   return up(p.blocks * cols * (int64_t)sizeof(float)) + up(stage_rows(p.blocks) * cols * (int64_t)sizeof(float));
 }
 
-template <typename T, typename C>
+// TY: the forward's output type, which is the backward's cotangent type
+template <typename T, typename TY, typename C>
 int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const NormPlan& p, void* dw, void* ws,
                 hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
@@ -441,8 +479,8 @@ int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const
   const C* n = static_cast<const C*>(sn);
   if (!backward) {
     if (p.blocks > 0)
-      hipLaunchKernelGGL((qk_norm_rope_fwd_kernel<T, C, VEC, 4>), dim3((unsigned)p.blocks), dim3(kThreads), 0, s, c,
-                         n, a);
+      hipLaunchKernelGGL((qk_norm_rope_fwd_kernel<T, TY, C, VEC, 4>), dim3((unsigned)p.blocks), dim3(kThreads), 0, s,
+                         c, n, a);
     return launched("pk_qk_norm_rope_fwd");
   }
   const int cols = 4 * a.half;
@@ -451,8 +489,8 @@ int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const
   float* stage = reinterpret_cast<float*>(static_cast<char*>(ws) + up(p.blocks * cols * (int64_t)sizeof(float)));
   if (p.blocks > 0) {
     const size_t lds = 4 * (size_t)(2 * a.half) * sizeof(float);
-    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, C, VEC, 2>), dim3((unsigned)p.blocks), dim3(kThreads), lds, s, c,
-                       n, a);
+    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, TY, C, VEC, 2>), dim3((unsigned)p.blocks), dim3(kThreads), lds, s,
+                       c, n, a);
     column_sums<T>(a.part, stage, static_cast<T*>(dw), p.blocks, cols, s);
   } else {  // nothing to sum: dw is zero
     hipLaunchKernelGGL(column_sum_final<T>, dim3((cols + kFinalCols - 1) / kFinalCols), dim3(kColThreads), 0, s,
@@ -513,21 +551,30 @@ int norm_setup(const char* who, NormArgs& a, NormPlan& p, const void* q, const v
   return PK_OK;
 }
 
-template <typename T> int norm_run_cs(int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
-                                      const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+template <typename T, typename TY>
+int norm_run_cs(int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a, const NormPlan& p,
+                void* dw, void* ws, hipStream_t s) {
   switch (cs_dtype) {
-    case PK_F32: return norm_launch<T, float>(backward, cs, sn, a, p, dw, ws, s);
-    case PK_BF16: return norm_launch<T, bf16>(backward, cs, sn, a, p, dw, ws, s);
-    default: return norm_launch<T, f16>(backward, cs, sn, a, p, dw, ws, s);
+    case PK_F32: return norm_launch<T, TY, float>(backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_launch<T, TY, bf16>(backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_launch<T, TY, f16>(backward, cs, sn, a, p, dw, ws, s);
   }
 }
 
-int norm_run(int x_dtype, int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
+// The output (or cotangent) type is x's, or fp32 with a 16-bit x.
+bool norm_pair(int x_dtype, int y_dtype) {
+  return known_dtype(x_dtype) && (y_dtype == x_dtype || (y_dtype == PK_F32 && x_dtype != PK_F32));
+}
+
+int norm_run(int x_dtype, int y_dtype, int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
              const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+  if (y_dtype != x_dtype)
+    return x_dtype == PK_BF16 ? norm_run_cs<bf16, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s)
+                              : norm_run_cs<f16, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
   switch (x_dtype) {
-    case PK_F32: return norm_run_cs<float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
-    case PK_BF16: return norm_run_cs<bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
-    default: return norm_run_cs<f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    case PK_F32: return norm_run_cs<float, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_run_cs<bf16, bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_run_cs<f16, f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
   }
 }
 
@@ -538,7 +585,7 @@ extern "C" {
 
 int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void* yq, void* yk,
             const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-            int64_t cos_batch, int x_dtype, int cs_dtype, int transpose, void* stream) {
+            int64_t cos_batch, int x_dtype, int y_dtype, int cs_dtype, int transpose, void* stream) {
   using namespace pk;
   if (batch < 0 || q_heads < 0 || kv_heads < 0 || seq < 0 || head_dim < 0)
     return fail(PK_ERR_INVALID, "pk_rope: negative size");
@@ -549,8 +596,8 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
   if (batch == 0 || seq == 0 || head_dim == 0 || q_heads + kv_heads == 0) return PK_OK;
   if (!cos || !sin || !strides || (q_heads > 0 && (!q || !yq)) || (kv_heads > 0 && (!k || !yk)))
     return fail(PK_ERR_INVALID, "pk_rope: null pointer");
-  if (!known_dtype(x_dtype) || !known_dtype(cs_dtype))
-    return fail(PK_ERR_UNSUPPORTED, "pk_rope: dtype codes %d/%d", x_dtype, cs_dtype);
+  if (!known_dtype(cs_dtype) || !rope_pair(x_dtype, y_dtype))
+    return fail(PK_ERR_UNSUPPORTED, "pk_rope: dtype codes %d -> %d with tables %d", x_dtype, y_dtype, cs_dtype);
   if (batch > INT32_MAX || seq > INT32_MAX || q_heads > INT32_MAX || kv_heads > INT32_MAX || head_dim > INT32_MAX)
     return fail(PK_ERR_UNSUPPORTED, "pk_rope: shape too large");
   if (q_heads + kv_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "pk_rope: too many heads");
@@ -571,29 +618,28 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
   a.seq = (int)seq;
   a.half = (int)(head_dim / 2);
   a.cos_batch = (int)cos_batch;
-  // 16-byte packs of x when every row start and both halves are 16-byte
-  // aligned (half a multiple of V and strides multiples of V); a pack's table
-  // entries are then 16-byte loads too whenever they fill whole 16 bytes,
-  // which needs only the table bases aligned.
-  const int64_t V = 16 / elem_size(x_dtype);
+  // 16-byte packs of the narrower of x and y when every row start and both
+  // halves are 16-byte aligned (half a multiple of V and strides multiples of
+  // V); a pack's table entries are then 16-byte loads too whenever they fill
+  // whole 16 bytes, which needs only the table bases aligned.
+  const int narrow = elem_size(x_dtype) < elem_size(y_dtype) ? elem_size(x_dtype) : elem_size(y_dtype);
+  const int64_t V = 16 / narrow;
   bool vec = a.half % V == 0;
   const void* ptrs[] = {q, k, yq, yk};
   for (const void* p : ptrs) vec = vec && (p == nullptr || aligned16(p));
   for (int i = 0; i < 12; ++i) vec = vec && strides[i] % V == 0;
   if ((V * elem_size(cs_dtype)) % 16 == 0) vec = vec && aligned16(cos) && aligned16(sin);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (x_dtype) {
-    case PK_F32: return run_cs<float>(cs_dtype, vec, cos, sin, a, transpose, s);
-    case PK_BF16: return run_cs<bf16>(cs_dtype, vec, cos, sin, a, transpose, s);
-    default: return run_cs<f16>(cs_dtype, vec, cos, sin, a, transpose, s);
-  }
+  return run_types(x_dtype, y_dtype, cs_dtype, vec, cos, sin, a, transpose, static_cast<hipStream_t>(stream));
 }
 
 int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
                         const void* sin, void* yq, void* yk, float* rstd_q, float* rstd_k, const int64_t* strides,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-                        int64_t cos_batch, float eps, int x_dtype, int cs_dtype, void* stream) {
+                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, void* stream) {
   using namespace pk;
+  if (!norm_pair(x_dtype, y_dtype))
+    return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_fwd: dtype codes %d -> %d (x's, or fp32 from 16 bits)", x_dtype,
+                y_dtype);
   NormArgs a;
   NormPlan p;
   int rc = norm_setup("pk_qk_norm_rope_fwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 12, batch, q_heads,
@@ -614,7 +660,8 @@ int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, cons
     a.ys[1][i] = strides[9 + i];
   }
   a.eps = eps;
-  return norm_run(x_dtype, cs_dtype, false, cos, sin, a, p, nullptr, nullptr, static_cast<hipStream_t>(stream));
+  return norm_run(x_dtype, y_dtype, cs_dtype, false, cos, sin, a, p, nullptr, nullptr,
+                  static_cast<hipStream_t>(stream));
 }
 
 int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
@@ -631,8 +678,11 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
                         const void* sin, const float* rstd_q, const float* rstd_k, const void* dyq, const void* dyk,
                         void* dq, void* dk, void* dw, void* workspace, int64_t workspace_bytes,
                         const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
-                        int64_t head_dim, int64_t cos_batch, int x_dtype, int cs_dtype, void* stream) {
+                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, void* stream) {
   using namespace pk;
+  if (!norm_pair(x_dtype, dy_dtype))
+    return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_bwd: dtype codes %d / %d (cotangents x's, or fp32 from 16 bits)",
+                x_dtype, dy_dtype);
   NormArgs a;
   NormPlan p;
   int rc = norm_setup("pk_qk_norm_rope_bwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 18, batch, q_heads,
@@ -664,7 +714,7 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
       a.ys[1][i] = strides[15 + i];
     }
   }
-  return norm_run(x_dtype, cs_dtype, true, cos, sin, a, p, dw, workspace, static_cast<hipStream_t>(stream));
+  return norm_run(x_dtype, dy_dtype, cs_dtype, true, cos, sin, a, p, dw, workspace, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -50,6 +50,28 @@ def _same_dtype(name: str, *tensors: Tensor | None) -> torch.dtype:
     return dtype
 
 
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _norm_dtypes(name: str, x: Tensor, weight: Tensor, bias: Tensor | None) -> tuple[torch.dtype, torch.dtype]:
+    """(x dtype, weight dtype): one dtype, or a 16-bit x with fp32 weight (and bias), whose product promotes to fp32."""
+    if bias is not None and bias.dtype != weight.dtype:
+        raise TypeError(f"popcorn_amd.{name}: bias dtype {bias.dtype} differs from weight dtype {weight.dtype}")
+    if x.dtype != weight.dtype and not (x.dtype in _HALF and weight.dtype == torch.float32):
+        raise TypeError(f"popcorn_amd.{name}: x {x.dtype} with weight {weight.dtype} is not supported "
+                        "(one dtype, or a 16-bit x with an fp32 weight)")
+    _lib.dtype_code(x.dtype)
+    _lib.dtype_code(weight.dtype)
+    return x.dtype, weight.dtype
+
+
+def _table_dtype(name: str, cos: Tensor, sin: Tensor) -> torch.dtype:
+    if cos.dtype != sin.dtype:
+        raise TypeError(f"popcorn_amd.{name}: cos {cos.dtype} and sin {sin.dtype} differ")
+    _lib.dtype_code(cos.dtype)
+    return cos.dtype
+
+
 # --------------------------------------------------------------------------- rms_norm
 
 
@@ -57,7 +79,7 @@ class _RMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, eps: float) -> Tensor:
         device = _require_cuda(x, weight, bias)
-        dtype = _same_dtype("rms_norm", x, weight, bias)
+        dtype, wdtype = _norm_dtypes("rms_norm", x, weight, bias)
         cols = x.shape[-1]
         if weight.shape != (cols,) or (bias is not None and bias.shape != (cols,)):
             raise ValueError(f"popcorn_amd.rms_norm: weight/bias must be [{cols}]")
@@ -65,7 +87,7 @@ class _RMSNorm(torch.autograd.Function):
         w = weight.contiguous()
         b = bias.contiguous() if bias is not None else None
         rows = x2.shape[0]
-        y = torch.empty_like(x2)
+        y = torch.empty(x2.shape, dtype=wdtype, device=device)
         rstd = torch.empty(rows, dtype=torch.float32, device=device)
         lib = _lib.load()
         _lib.check(
@@ -79,6 +101,7 @@ class _RMSNorm(torch.autograd.Function):
                 cols,
                 float(eps),
                 _lib.dtype_code(dtype),
+                _lib.dtype_code(wdtype),
                 _lib.stream_handle(device),
             ),
             lib,
@@ -92,7 +115,7 @@ class _RMSNorm(torch.autograd.Function):
     def backward(ctx, dy: Tensor):
         x2, w, rstd = ctx.saved_tensors
         rows, cols = x2.shape
-        dy2 = dy.reshape(rows, cols).to(x2.dtype).contiguous()
+        dy2 = dy.reshape(rows, cols).to(w.dtype).contiguous()
         dx = torch.empty_like(x2)
         dw = torch.empty_like(w)
         db = torch.empty_like(w) if ctx.has_bias else None
@@ -119,6 +142,7 @@ class _RMSNorm(torch.autograd.Function):
                     rows,
                     cols,
                     code,
+                    _lib.dtype_code(w.dtype),
                     _lib.stream_handle(x2.device),
                 ),
                 lib,
@@ -130,7 +154,10 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
     """y = round(round(x * rsqrt(mean(x^2) + eps)) * weight) [+ bias], fp32 statistics.
 
     x [..., normalized_shape]; weight, bias [normalized_shape]; one dtype for all
-    (fp32, bf16 or fp16). Backward gives dx, dweight, dbias.
+    (fp32, bf16 or fp16), or a 16-bit x with fp32 weight and bias, where the
+    normalized x is rounded to x's dtype and the output promotes to fp32
+    (kernels/rms_norm.py:29). Backward gives dx (x's dtype), dweight, dbias
+    (the weight's).
     """
     return _RMSNorm.apply(x, weight, bias, eps)
 
@@ -335,11 +362,17 @@ def rotary_embedding_(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = F
     return x
 
 
-def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpose: bool):
-    """One pk_rope launch over whichever of q, k is given; returns (yq, yk) (None for an absent side)."""
+def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpose: bool,
+          out_dtype: torch.dtype | None = None):
+    """One pk_rope launch over whichever of q, k is given; returns (yq, yk) (None for an absent side).
+
+    The outputs have `out_dtype`, by default q/k's dtype promoted with the tables'.
+    """
     sides = [t for t in (q, k) if t is not None]
     device = _require_cuda(*sides, cos, sin)
-    dtype = _same_dtype("rope", *sides, cos, sin)
+    dtype = _same_dtype("rope", *sides)
+    cs_dtype = _table_dtype("rope", cos, sin)
+    out_dtype = torch.promote_types(dtype, cs_dtype) if out_dtype is None else out_dtype
     if any(t.dim() != 4 for t in sides) or cos.dim() != 3 or cos.shape != sin.shape:
         raise ValueError("popcorn_amd.rope: q [b, hq, s, d], k [b, hkv, s, d] and cos, sin [cos_batch, s, d] expected")
     batch, _, seq, head_dim = sides[0].shape
@@ -351,7 +384,7 @@ def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpos
     if head_dim % 2:
         raise ValueError(f"popcorn_amd.rope: head_dim={head_dim} is odd")
     xq, xk = (None if t is None else _last_contiguous(t.detach()) for t in (q, k))
-    yq, yk = (None if t is None else torch.empty(t.shape, dtype=dtype, device=device) for t in (q, k))
+    yq, yk = (None if t is None else torch.empty(t.shape, dtype=out_dtype, device=device) for t in (q, k))
     cs, sn = cos.detach().contiguous(), sin.detach().contiguous()
 
     def strides(t):
@@ -364,7 +397,8 @@ def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpos
         lib.pk_rope(
             ptr(xq), ptr(xk), cs.data_ptr(), sn.data_ptr(), ptr(yq), ptr(yk), st, batch,
             0 if q is None else q.shape[1], 0 if k is None else k.shape[1], seq, head_dim, cos.shape[0],
-            _lib.dtype_code(dtype), _lib.dtype_code(dtype), int(transpose), _lib.stream_handle(device),
+            _lib.dtype_code(dtype), _lib.dtype_code(out_dtype), _lib.dtype_code(cs_dtype), int(transpose),
+            _lib.stream_handle(device),
         ),
         lib,
     )
@@ -376,6 +410,7 @@ class _Rope(torch.autograd.Function):
     def forward(ctx, q: Tensor, k: Tensor, cos: Tensor, sin: Tensor):
         yq, yk = _rope(q, k, cos, sin, transpose=False)
         ctx.save_for_backward(cos.detach().contiguous(), sin.detach().contiguous())
+        ctx.dtypes = q.dtype, yq.dtype
         return yq, yk
 
     @staticmethod
@@ -383,7 +418,9 @@ class _Rope(torch.autograd.Function):
         cos, sin = ctx.saved_tensors
         if gq is None and gk is None:
             return None, None, None, None
-        dq, dk = _rope(gq, gk, cos, sin, transpose=True)
+        x_dtype, y_dtype = ctx.dtypes
+        gq, gk = (None if g is None else g.to(y_dtype) for g in (gq, gk))
+        dq, dk = _rope(gq, gk, cos, sin, transpose=True, out_dtype=x_dtype)
         return dq, dk, None, None
 
 
@@ -391,16 +428,19 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
     """Paired rotary embedding: (q*cos + rotate_half(q)*sin, k*cos + rotate_half(k)*sin).
 
     q [batch, q_heads, seq, head_dim], k [batch, kv_heads, seq, head_dim],
-    cos, sin [cos_batch, seq, head_dim] with cos_batch 1 or batch, all one
-    dtype; the two halves of a table row may differ. fp32 arithmetic, one
-    rounding per output; one launch for q and k. cos and sin get no gradient.
+    cos, sin [cos_batch, seq, head_dim] with cos_batch 1 or batch; q, k one
+    dtype and cos, sin one dtype, the outputs their promotion (16-bit q/k with
+    fp32 tables give fp32, kernels/rope.py:35-36). The two halves of a table
+    row may differ. fp32 arithmetic, one rounding per output; one launch for q
+    and k. Gradients have q/k's dtype; cos and sin get none.
     """
     return _Rope.apply(q, k, cos, sin)
 
 
 def _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin):
     device = _require_cuda(q, k, q_weight, k_weight, cos, sin)
-    dtype = _same_dtype("qk_norm_rope", q, k, q_weight, k_weight, cos, sin)
+    dtype = _same_dtype("qk_norm_rope", q, k, q_weight, k_weight)
+    _table_dtype("qk_norm_rope", cos, sin)
     if q.dim() != 4 or k.dim() != 4 or cos.dim() != 3 or cos.shape != sin.shape:
         raise ValueError("popcorn_amd.qk_norm_rope: q [b, hq, s, d], k [b, hkv, s, d], cos, sin [cb, s, d] expected")
     batch, _, seq, head_dim = q.shape
@@ -425,7 +465,9 @@ class _QkNormRope(torch.autograd.Function):
         device, dtype, batch, seq, head_dim = _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin)
         q_, k_ = _aligned_rows(q.detach()), _aligned_rows(k.detach())
         qw, kw, cs, sn = (_dense(t) for t in (q_weight, k_weight, cos, sin))
-        yq, yk = torch.empty(q.shape, dtype=dtype, device=device), torch.empty(k.shape, dtype=dtype, device=device)
+        out_dtype = torch.promote_types(dtype, cs.dtype)
+        yq = torch.empty(q.shape, dtype=out_dtype, device=device)
+        yk = torch.empty(k.shape, dtype=out_dtype, device=device)
         rq = torch.empty((batch, q.shape[1], seq), dtype=torch.float32, device=device)
         rk = torch.empty((batch, k.shape[1], seq), dtype=torch.float32, device=device)
         lib = _lib.load()
@@ -435,19 +477,22 @@ class _QkNormRope(torch.autograd.Function):
             lib.pk_qk_norm_rope_fwd(
                 q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
                 yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
-                head_dim, cos.shape[0], float(eps), code, code, _lib.stream_handle(device),
+                head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
+                _lib.stream_handle(device),
             ),
             lib,
         )
         ctx.save_for_backward(q_, k_, qw, kw, cs, sn, rq, rk)
+        ctx.out_dtype = out_dtype
         return yq, yk
 
     @staticmethod
     def backward(ctx, gq, gk):
         q_, k_, qw, kw, cs, sn, rq, rk = ctx.saved_tensors
         batch, _, seq, head_dim = q_.shape
-        gq = torch.zeros_like(q_) if gq is None else _aligned_rows(gq.to(q_.dtype))
-        gk = torch.zeros_like(k_) if gk is None else _aligned_rows(gk.to(k_.dtype))
+        gdt = ctx.out_dtype
+        gq = torch.zeros(q_.shape, dtype=gdt, device=q_.device) if gq is None else _aligned_rows(gq.to(gdt))
+        gk = torch.zeros(k_.shape, dtype=gdt, device=k_.device) if gk is None else _aligned_rows(gk.to(gdt))
         dq, dk = torch.empty(q_.shape, dtype=q_.dtype, device=q_.device), torch.empty(k_.shape, dtype=k_.dtype,
                                                                                        device=k_.device)
         dw = torch.empty((2, head_dim), dtype=q_.dtype, device=q_.device)
@@ -463,7 +508,7 @@ class _QkNormRope(torch.autograd.Function):
                 q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
                 rq.data_ptr(), rk.data_ptr(), gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                 dw.data_ptr(), ws.data_ptr(), nbytes, st, batch, q_.shape[1], k_.shape[1], seq, head_dim,
-                cs.shape[0], code, code, _lib.stream_handle(q_.device),
+                cs.shape[0], code, _lib.dtype_code(gdt), _lib.dtype_code(cs.dtype), _lib.stream_handle(q_.device),
             ),
             lib,
         )
@@ -475,10 +520,12 @@ def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, cos: 
     """Per-head RMSNorm of q and k (weights over head_dim), then `rope`, fused into one pass.
 
     q [batch, q_heads, seq, head_dim], k [batch, kv_heads, seq, head_dim],
-    q_weight, k_weight [head_dim], cos, sin [cos_batch, seq, head_dim], all one
-    dtype; head_dim / 2 a 16-byte pack count times a power of two up to 64.
-    fp32 arithmetic, one rounding per output. Backward gives dq, dk and the
-    two weight gradients; cos and sin get none.
+    q_weight, k_weight [head_dim], cos, sin [cos_batch, seq, head_dim]; q, k and
+    the weights one dtype, cos and sin one dtype, the outputs their promotion
+    (16-bit q/k with fp32 tables give fp32); head_dim / 2 a 16-byte pack count
+    (of q's dtype) times a power of two up to 64. fp32 arithmetic, one rounding
+    per output. Backward gives dq, dk and the two weight gradients in q's
+    dtype; cos and sin get none.
     """
     return _QkNormRope.apply(q, k, q_weight, k_weight, cos, sin, eps)
 

@@ -48,8 +48,11 @@ def gauge_ok(mine, truth, ref_native, dtype: torch.dtype, what: str = "out") -> 
     return {"err": err, "budget": budget, "scale": scale}
 
 
-def close_to_reference(mine: torch.Tensor, ref: torch.Tensor, what: str = "out") -> None:
-    rtol, atol = NORTH_STAR[ref.dtype]
+def close_to_reference(mine: torch.Tensor, ref: torch.Tensor, what: str = "out",
+                       rounding: torch.dtype | None = None) -> None:
+    """`rounding`: the dtype whose tolerance applies when an fp32 output carries a 16-bit rounding
+    (a 16-bit input promoted by an fp32 operand); by default the output's own dtype."""
+    rtol, atol = NORTH_STAR[ref.dtype if rounding is None else rounding]
     torch.testing.assert_close(mine.detach().cpu(), ref.detach().cpu(), rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
 
 

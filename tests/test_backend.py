@@ -44,3 +44,30 @@ def test_cpu_tensors_are_declined_and_torch_serves():
     op = compat.KERNELS["rms_norm"]
     assert op[backend.BACKEND].refusal(describe(op, (x, w), {}))
     torch.testing.assert_close(op(x, w), compat.references.rms_norm(x, w))
+
+
+def test_predicates_cover_the_mixed_dtype_pairs(monkeypatch):
+    """Mixed pairs the kernels implement are accepted; the rest are declined (placement aside, on meta tensors)."""
+    monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
+    bf, f16, f32 = torch.bfloat16, torch.float16, torch.float32
+
+    def t(*shape, dtype):
+        return torch.empty(shape, dtype=dtype, device="meta")
+
+    x = t(4, 64, dtype=bf)
+    assert backend.rms_norm_supported(x, t(64, dtype=f32), None, 1e-6)
+    assert backend.rms_norm_supported(x, t(64, dtype=f32), t(64, dtype=f32), 1e-6)
+    assert not backend.rms_norm_supported(x, t(64, dtype=f32), t(64, dtype=bf), 1e-6)
+    assert not backend.rms_norm_supported(t(4, 64, dtype=f32), t(64, dtype=bf), None, 1e-6)
+    assert not backend.rms_norm_supported(x, t(64, dtype=f16), None, 1e-6)
+
+    q, k = t(2, 4, 8, 64, dtype=bf), t(2, 2, 8, 64, dtype=bf)
+    for table in (bf, f16, f32):
+        cs = t(1, 8, 64, dtype=table)
+        assert backend.rope_supported(q, k, cs, cs)
+        w = t(64, dtype=bf)
+        assert backend.qk_norm_rope_supported(q, k, w, w, cs, cs, 1e-6)
+    assert not backend.rope_supported(q, t(2, 2, 8, 64, dtype=f16), t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=f32))
+    assert not backend.rope_supported(q, k, t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=bf))
+    w32 = t(64, dtype=f32)
+    assert not backend.qk_norm_rope_supported(q, k, w32, w32, t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=f32), 1e-6)

@@ -75,7 +75,7 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     assert "negative size" in lib.pk_last_error().decode()
     assert lib.pk_swiglu_fwd(None, None, None, 0, _lib.BF16, None) == _lib.OK  # empty: nothing to do
     assert lib.pk_swiglu_fwd(None, None, None, 8, 7, None) in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED)
-    assert lib.pk_rmsnorm_fwd(None, None, None, None, None, -1, 8, 1e-6, _lib.F32, None) == _lib.ERR_INVALID
+    assert lib.pk_rmsnorm_fwd(None, None, None, None, None, -1, 8, 1e-6, _lib.F32, _lib.F32, None) == _lib.ERR_INVALID
     assert lib.pk_rmsnorm_bwd_workspace(0, 8, _lib.BF16) == 0
     assert lib.pk_rmsnorm_bwd_workspace(4096, 8192, _lib.BF16) > 0
     strides = (ctypes.c_int64 * 12)(*([8] * 12))
@@ -92,13 +92,22 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, 9, None)
     assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
     rs = (ctypes.c_int64 * 12)(*([64] * 12))
-    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 63, 1, _lib.BF16, _lib.BF16, 0, None)
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 63, 1, _lib.BF16, _lib.BF16, _lib.BF16, 0, None)
     assert rc == _lib.ERR_INVALID and "odd" in lib.pk_last_error().decode()
-    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 3, _lib.BF16, _lib.BF16, 0, None)
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 3, _lib.BF16, _lib.BF16, _lib.BF16, 0, None)
     assert rc == _lib.ERR_INVALID and "cos_batch" in lib.pk_last_error().decode()
-    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 2, _lib.BF16, _lib.BF16, 0, None)
+    rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 2, _lib.BF16, _lib.BF16, _lib.BF16, 0, None)
     assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
-    assert lib.pk_rope(None, None, None, None, None, None, rs, 2, 0, 0, 8, 64, 1, _lib.BF16, _lib.BF16, 0, None) == 0
+    assert lib.pk_rope(None, None, None, None, None, None, rs, 2, 0, 0, 8, 64, 1, _lib.BF16, _lib.BF16, _lib.BF16, 0, None) == 0
+    # dtype pairs: one dtype, or a 16-bit side beside fp32 (rope); x's, or fp32 from 16 bits (qk_norm_rope)
+    fake = ctypes.c_void_p(16)
+    rc = lib.pk_rope(fake, fake, fake, fake, fake, fake, rs, 2, 4, 2, 8, 64, 1, _lib.BF16, _lib.F16, _lib.F32, 0, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
+    rc = lib.pk_qk_norm_rope_fwd(None, None, None, None, None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 1,
+                                 1e-6, _lib.F32, _lib.BF16, _lib.F32, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
+    rc = lib.pk_rmsnorm_fwd(fake, fake, None, fake, None, 4, 64, 1e-6, _lib.F32, _lib.BF16, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "weight dtype" in lib.pk_last_error().decode()
 
 
 def test_missing_library_raises(tmp_path):

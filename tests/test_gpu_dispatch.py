@@ -172,6 +172,24 @@ def test_mixed_dtype_rotary_is_served_in_registration_order():
     assert torch.equal(y, impls.rotary_embedding(x, cos, sin))
 
 
+def test_mixed_dtype_rms_norm_and_rope_are_served_by_the_backend():
+    """16-bit activations with fp32 weights or tables (the autocast model's calls) reach the kernels."""
+    x = _randn(64, 1024)
+    w = 1 + 0.1 * torch.randn(1024, device=DEV)
+    op = compat.KERNELS["rms_norm"]
+    y = op(x, w)
+    assert _selected(op) == NAME and y.dtype == torch.float32
+    assert torch.equal(y, impls.rms_norm(x, w))
+    q, k = _randn(1, 4, 32, 128), _randn(1, 2, 32, 128, seed=1)
+    ang = torch.randn(1, 32, 64, device=DEV)
+    cos, sin = ang.cos().repeat(1, 1, 2), ang.sin().repeat(1, 1, 2)
+    op = compat.KERNELS["rope"]
+    yq, yk = op(q, k, cos, sin)
+    assert _selected(op) == NAME and yq.dtype == yk.dtype == torch.float32
+    want = impls.rope(q, k, cos, sin)
+    assert torch.equal(yq, want[0]) and torch.equal(yk, want[1])
+
+
 def test_bench_mode_measures_lazily(monkeypatch):
     op = compat.KERNELS["swiglu"]
     monkeypatch.setenv("POPCORN_BENCH", "1")

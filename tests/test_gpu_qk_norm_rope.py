@@ -25,13 +25,16 @@ def tables(cos_batch, seq, head_dim, seed, duplicated=True):
     return draw.cos(), seeded((cos_batch, seq, head_dim), seed + 1, torch.float32).sin()
 
 
-def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicated=True):
+def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicated=True, table_dtype=None):
+    """q, k, weights in `dtype`, tables in `table_dtype` (default `dtype`); outputs and cotangents in their promotion."""
+    table_dtype = dtype if table_dtype is None else table_dtype
+    out_dtype = torch.promote_types(dtype, table_dtype)
     q = seeded((batch, hq, seq, d), seed, dtype)
     k = seeded((batch, hkv, seq, d), seed + 1, dtype)
     qw = seeded((d,), seed + 6, dtype)
     kw = seeded((d,), seed + 7, dtype)
-    cos, sin = (t.to(dtype) for t in tables(cos_batch, seq, d, seed + 2, duplicated))
-    gq, gk = seeded(tuple(q.shape), seed + 4, dtype), seeded(tuple(k.shape), seed + 5, dtype)
+    cos, sin = (t.to(table_dtype) for t in tables(cos_batch, seq, d, seed + 2, duplicated))
+    gq, gk = seeded(tuple(q.shape), seed + 4, out_dtype), seeded(tuple(k.shape), seed + 5, out_dtype)
     n64 = lambda t: t.double().numpy()  # noqa: E731
     y64 = O.qk_norm_rope(n64(q), n64(k), n64(qw), n64(kw), n64(cos), n64(sin), eps)
     d64 = O.qk_norm_rope_bwd(n64(q), n64(k), n64(qw), n64(kw), n64(cos), n64(sin), n64(gq), n64(gk), eps)
@@ -44,10 +47,11 @@ def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicate
     what = f"(b {batch}, hq {hq}, hkv {hkv}, s {seq}, d {d}, cos_batch {cos_batch}, eps {eps})"
     names = ("yq", "yk", "dq", "dk", "dq_weight", "dk_weight")
     for name, got, truth, ref in zip(names, (*ym, *dm), (*y64, *d64), (*yr, *dr)):
-        assert got.shape == ref.shape and got.dtype == dtype, name
-        gauge_ok(got, truth, ref, dtype, f"{name} {what}")
+        want = out_dtype if name.startswith("y") else dtype
+        assert got.shape == ref.shape and got.dtype == ref.dtype == want, name
+        gauge_ok(got, truth, ref, want, f"{name} {what}")
     for name, got, ref in zip(("yq", "yk"), ym, yr):
-        close_to_reference(got, ref, f"{name} {what}")
+        close_to_reference(got, ref, f"{name} {what}", rounding=dtype)
 
 
 CASES = [
@@ -65,6 +69,13 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=str)
 def test_qk_norm_rope(case, dtype):
     _check(*case, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", CASES, ids=str)
+def test_qk_norm_rope_fp32_tables(case, dtype):
+    """16-bit q/k and weights with fp32 tables: fp32 outputs (and cotangents), 16-bit gradients."""
+    _check(*case, dtype, table_dtype=torch.float32)
 
 
 @pytest.mark.parametrize("case", [(2, 4, 2, 16, 128, 1), (1, 3, 1, 9, 8, 1), (2, 2, 1, 40, 64, 2)], ids=str)

@@ -23,12 +23,14 @@ def _weights(cols, dtype, seed):
     return (1 + 0.1 * seeded((cols,), seed, torch.float32)).to(dtype)
 
 
-def _run(shape, dtype, eps, with_bias, seed):
+def _run(shape, dtype, eps, with_bias, seed, wdtype=None):
+    """x in `dtype`; weight, bias, the output and its cotangent in `wdtype` (default `dtype`)."""
+    wdtype = dtype if wdtype is None else wdtype
     cols = shape[-1]
     x = seeded(shape, seed, dtype)
-    w = _weights(cols, dtype, seed + 1)
-    bias = seeded((cols,), seed + 2, dtype) if with_bias else None
-    g = seeded(shape, 1000 + seed, dtype)
+    w = _weights(cols, wdtype, seed + 1)
+    bias = seeded((cols,), seed + 2, wdtype) if with_bias else None
+    g = seeded(shape, 1000 + seed, wdtype)
 
     b64 = bias.double().numpy() if with_bias else None
     y64 = O.rms_norm(x.double().numpy(), w.double().numpy(), b64, eps)
@@ -44,13 +46,14 @@ def _run(shape, dtype, eps, with_bias, seed):
     ym = impls.rms_norm(mine[0], mine[1], mine[2] if with_bias else None, eps)
     grads_m = torch.autograd.grad(ym, mine, g.to(DEV))
 
-    assert ym.shape == x.shape and ym.dtype == dtype
-    gauge_ok(ym, y64, yr, dtype, "y")
-    close_to_reference(ym, yr, "y")
+    assert ym.shape == x.shape and ym.dtype == yr.dtype == wdtype
+    assert [t.dtype for t in grads_m] == [t.dtype for t in grads_r]
+    gauge_ok(ym, y64, yr, wdtype, "y")
+    close_to_reference(ym, yr, "y", rounding=dtype)
     gauge_ok(grads_m[0], dx64, grads_r[0], dtype, "dx")
-    gauge_ok(grads_m[1], dw64, grads_r[1], dtype, "dw")
+    gauge_ok(grads_m[1], dw64, grads_r[1], wdtype, "dw")
     if with_bias:
-        gauge_ok(grads_m[2], db64, grads_r[2], dtype, "db")
+        gauge_ok(grads_m[2], db64, grads_r[2], wdtype, "db")
 
 
 # (3000, 4096) and (9001, 256) run the persistent forward grid over several
@@ -70,6 +73,28 @@ def test_rmsnorm(shape, dtype):
 @pytest.mark.parametrize("shape", [(4, 4096), (3, 1000), (64, 8192)], ids=str)
 def test_rmsnorm_bias_eps(shape, dtype):
     _run(shape, dtype, 1e-5, True, 3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", [(4, 4096), (3, 1000), (17, 8192), (2, 3, 512), (1, 7), (5, 16384), (3000, 4096),
+                                   (9001, 256)], ids=str)
+def test_rmsnorm_16bit_x_fp32_weight(shape, dtype):
+    """16-bit x with an fp32 weight (kernels/rms_norm.py:29): the normalized x rounds to x's dtype, the
+    product promotes to fp32; dx has x's dtype, dweight fp32."""
+    _run(shape, dtype, 1e-6, False, 5, wdtype=torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+def test_rmsnorm_16bit_x_fp32_weight_and_bias(dtype):
+    _run((64, 8192), dtype, 1e-5, True, 7, wdtype=torch.float32)
+
+
+def test_rmsnorm_mixed_pair_outside_the_kernels_raises():
+    x = torch.zeros(2, 64, dtype=torch.float32, device=DEV)
+    with pytest.raises(TypeError, match="not supported"):
+        impls.rms_norm(x, torch.ones(64, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(TypeError, match="bias dtype"):
+        impls.rms_norm(x.bfloat16(), torch.ones(64, device=DEV), torch.ones(64, dtype=torch.bfloat16, device=DEV))
 
 
 def test_rmsnorm_zero_rows_and_empty():

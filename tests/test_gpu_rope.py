@@ -28,11 +28,14 @@ def tables(cos_batch, seq, head_dim, seed, duplicated=True):
     return draw.cos(), seeded((cos_batch, seq, head_dim), seed + 1, torch.float32).sin()
 
 
-def _check(batch, hq, hkv, seq, d, cos_batch, dtype, seed=0, duplicated=True):
+def _check(batch, hq, hkv, seq, d, cos_batch, dtype, seed=0, duplicated=True, table_dtype=None):
+    """q, k in `dtype`, tables in `table_dtype` (default `dtype`); outputs and cotangents in their promotion."""
+    table_dtype = dtype if table_dtype is None else table_dtype
+    out_dtype = torch.promote_types(dtype, table_dtype)
     q = seeded((batch, hq, seq, d), seed, dtype)
     k = seeded((batch, hkv, seq, d), seed + 1, dtype)
-    cos, sin = (t.to(dtype) for t in tables(cos_batch, seq, d, seed + 2, duplicated))
-    gq, gk = seeded(tuple(q.shape), seed + 4, dtype), seeded(tuple(k.shape), seed + 5, dtype)
+    cos, sin = (t.to(table_dtype) for t in tables(cos_batch, seq, d, seed + 2, duplicated))
+    gq, gk = seeded(tuple(q.shape), seed + 4, out_dtype), seeded(tuple(k.shape), seed + 5, out_dtype)
     n64 = lambda t: t.double().numpy()  # noqa: E731
     y64 = O.rope(n64(q), n64(k), n64(cos), n64(sin))
     d64 = O.rope_bwd(n64(gq), n64(gk), n64(cos), n64(sin))
@@ -42,10 +45,11 @@ def _check(batch, hq, hkv, seq, d, cos_batch, dtype, seed=0, duplicated=True):
     qm, km = q.to(DEV).requires_grad_(), k.to(DEV).requires_grad_()
     ym = impls.rope(qm, km, cos.to(DEV), sin.to(DEV))
     dm = torch.autograd.grad(ym, (qm, km), (gq.to(DEV), gk.to(DEV)))
-    what = f"(b {batch}, hq {hq}, hkv {hkv}, s {seq}, d {d}, cos_batch {cos_batch})"
+    what = f"(b {batch}, hq {hq}, hkv {hkv}, s {seq}, d {d}, cos_batch {cos_batch}, tables {table_dtype})"
     for name, mine, truth, ref in zip(("yq", "yk", "dq", "dk"), (*ym, *dm), (*y64, *d64), (*yr, *dr)):
-        assert mine.shape == ref.shape and mine.dtype == dtype, name
-        gauge_ok(mine, truth, ref, dtype, f"{name} {what}")
+        want = out_dtype if name.startswith("y") else dtype
+        assert mine.shape == ref.shape and mine.dtype == ref.dtype == want, name
+        gauge_ok(mine, truth, ref, want, f"{name} {what}")
     for name, mine, ref in zip(("yq", "yk"), ym, yr):
         close_to_reference(mine, ref, f"{name} {what}")
     return ym
@@ -66,6 +70,21 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=str)
 def test_rope(case, dtype):
     _check(*case, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", CASES, ids=str)
+def test_rope_fp32_tables(case, dtype):
+    """16-bit q/k with fp32 tables (the model's fp32 cos/sin buffers): fp32 outputs, 16-bit gradients."""
+    _check(*case, dtype, table_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("pair", [(torch.bfloat16, torch.float16), (torch.float16, torch.bfloat16),
+                                  (torch.float32, torch.bfloat16)], ids=str)
+def test_rope_other_table_dtypes(pair):
+    """Tables of another dtype: the outputs take the promotion (fp32 for bf16 beside fp16)."""
+    dtype, table_dtype = pair
+    _check(2, 4, 2, 16, 128, 1, dtype, seed=9, table_dtype=table_dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
@@ -112,7 +131,7 @@ def test_rope_fp32_tables_with_bf16_inputs_through_the_c_abi():
     lib = _lib.load()
     st = (ctypes.c_int64 * 12)(*(x for t in (q, k, yq, yk) for x in t.stride()[:3]))
     _lib.check(lib.pk_rope(q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(), yq.data_ptr(), yk.data_ptr(),
-                           st, b, hq, hkv, s, d, b, _lib.BF16, _lib.F32, 0, _lib.stream_handle(q.device)), lib)
+                           st, b, hq, hkv, s, d, b, _lib.BF16, _lib.BF16, _lib.F32, 0, _lib.stream_handle(q.device)), lib)
     want = O.rope(q.cpu().double().numpy(), k.cpu().double().numpy(), cos.cpu().double().numpy(),
                   sin.cpu().double().numpy())
     for got, w in zip((yq, yk), want):

@@ -34,33 +34,36 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
-def _inputs(rows, cols, dtype, seed, with_bias):
+def _inputs(rows, cols, dtype, seed, with_bias, wdtype=None):
+    """x in `dtype`; weight, bias and the cotangent dy in `wdtype` (default `dtype`)."""
+    wdtype = dtype if wdtype is None else wdtype
     x = seeded((rows, cols), seed, dtype).to(DEV)
-    w = (1 + 0.1 * seeded((cols,), seed + 1, torch.float32)).to(dtype).to(DEV)
-    dy = seeded((rows, cols), seed + 2, dtype).to(DEV)
-    bias = seeded((cols,), seed + 3, dtype).to(DEV) if with_bias else None
+    w = (1 + 0.1 * seeded((cols,), seed + 1, torch.float32)).to(wdtype).to(DEV)
+    dy = seeded((rows, cols), seed + 2, wdtype).to(DEV)
+    bias = seeded((cols,), seed + 3, wdtype).to(DEV) if with_bias else None
     return x, w, dy, bias
 
 
-def _forward_rstd(lib, x, w, bias, rows, cols, code, stream):
-    y = torch.empty_like(x)
+def _forward_rstd(lib, x, w, bias, rows, cols, code, wcode, stream):
+    y = torch.empty(x.shape, dtype=w.dtype, device=DEV)
     rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
-    _lib.check(lib.pk_rmsnorm_fwd(_ptr(x), _ptr(w), _ptr(bias), _ptr(y), _ptr(rstd), rows, cols, 1e-6, code, stream),
+    _lib.check(lib.pk_rmsnorm_fwd(_ptr(x), _ptr(w), _ptr(bias), _ptr(y), _ptr(rstd), rows, cols, 1e-6, code, wcode,
+                                  stream),
                lib)
     return rstd
 
 
-def _backward_with_workspace(lib, x, w, rstd, dy, with_bias, rows, cols, code, stream):
+def _backward_with_workspace(lib, x, w, rstd, dy, with_bias, rows, cols, code, wcode, stream):
     dx, dw = torch.empty_like(x), torch.empty_like(w)
     db = torch.empty_like(w) if with_bias else None
     nbytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, code)
     work = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     _lib.check(lib.pk_rmsnorm_bwd(_ptr(x), _ptr(w), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(work),
-                                  nbytes, rows, cols, code, stream), lib)
+                                  nbytes, rows, cols, code, wcode, stream), lib)
     return dx, dw, db
 
 
-def _backward_noalloc(lib, x, w, rstd, dy, with_bias, rows, cols, code, stream):
+def _backward_noalloc(lib, x, w, rstd, dy, with_bias, rows, cols, code, wcode, stream):
     dx, dw = torch.empty_like(x), torch.empty_like(w)
     db = torch.empty_like(w) if with_bias else None
     # poison the outputs so a skipped write cannot pass as a match
@@ -68,7 +71,7 @@ def _backward_noalloc(lib, x, w, rstd, dy, with_bias, rows, cols, code, stream):
         if t is not None:
             t.fill_(float("nan"))
     _lib.check(lib.pk_rmsnorm_bwd_noalloc(_ptr(x), _ptr(w), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db),
-                                          rows, cols, code, stream), lib)
+                                          rows, cols, code, wcode, stream), lib)
     return dx, dw, db
 
 
@@ -76,14 +79,15 @@ def _bits(t):
     return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
 
 
-def _compare(lib, rows, cols, dtype, seed, with_bias):
-    code = _lib.dtype_code(dtype)
+def _compare(lib, rows, cols, dtype, seed, with_bias, wdtype=None):
+    wdtype = dtype if wdtype is None else wdtype
+    code, wcode = _lib.dtype_code(dtype), _lib.dtype_code(wdtype)
     stream = _lib.stream_handle(torch.device(DEV))
-    print(f"[noalloc] rows={rows} cols={cols} dtype={dtype} bias={with_bias}", flush=True)
-    x, w, dy, bias = _inputs(rows, cols, dtype, seed, with_bias)
-    rstd = _forward_rstd(lib, x, w, bias, rows, cols, code, stream)
-    ref = _backward_with_workspace(lib, x, w, rstd, dy, with_bias, rows, cols, code, stream)
-    mine = _backward_noalloc(lib, x, w, rstd, dy, with_bias, rows, cols, code, stream)
+    print(f"[noalloc] rows={rows} cols={cols} dtype={dtype} weight={wdtype} bias={with_bias}", flush=True)
+    x, w, dy, bias = _inputs(rows, cols, dtype, seed, with_bias, wdtype)
+    rstd = _forward_rstd(lib, x, w, bias, rows, cols, code, wcode, stream)
+    ref = _backward_with_workspace(lib, x, w, rstd, dy, with_bias, rows, cols, code, wcode, stream)
+    mine = _backward_noalloc(lib, x, w, rstd, dy, with_bias, rows, cols, code, wcode, stream)
     torch.cuda.synchronize()
     for name, a, b in zip(("dx", "dw", "db"), mine, ref):
         if b is None:
@@ -113,6 +117,8 @@ def test_noalloc_other_dtypes_bias_and_row_widths(lib):
     _compare(lib, 1030, 1000, torch.float16, 2, True)  # unaligned width: the one-block-per-row kernels
     _compare(lib, 9001, 256, torch.bfloat16, 3, True)  # four rows per block
     _compare(lib, 17, 8192, torch.float32, 4, True)
+    _compare(lib, 4096, 8192, torch.bfloat16, 5, False, torch.float32)  # 16-bit x, fp32 weight and dy
+    _compare(lib, 1030, 1000, torch.float16, 6, True, torch.float32)
 
 
 def test_noalloc_refuses_a_shape_beyond_the_array(lib):
@@ -122,6 +128,6 @@ def test_noalloc_refuses_a_shape_beyond_the_array(lib):
     # 4096 rows of 2^18 fp32 columns: a partial row is 1 MiB, and the grid holds
     # at least one block per CU (256), so 256 MiB of partials: refused before any launch.
     rc = lib.pk_rmsnorm_bwd_noalloc(_ptr(x), _ptr(w), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db),
-                                    4096, 1 << 18, _lib.F32, _lib.stream_handle(torch.device(DEV)))
+                                    4096, 1 << 18, _lib.F32, _lib.F32, _lib.stream_handle(torch.device(DEV)))
     assert rc == _lib.ERR_UNSUPPORTED
     assert "scratch" in lib.pk_last_error().decode()
