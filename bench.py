@@ -530,20 +530,29 @@ def _time_cpu(fn, budget_s: float = 5.0, min_reps: int = 2, max_reps: int = 20) 
     return times[len(times) // 2], reps
 
 
-def _time_gpu(fn: Callable[[int], None], steps: int, warmup: int) -> tuple[float, list[float]]:
-    """Total ms for `steps` back-to-back calls and each call's ms, from HIP events on torch's current stream."""
+def _time_gpu(fn: Callable[[int], None], steps: int, warmup: int) -> float:
+    """Total ms of `steps` back-to-back calls, between two HIP events on torch's current stream.
+
+    The calls run with nothing between them: an event recorded between two
+    launches costs the GPU several microseconds of idle time, which would be
+    charged to kernels of a few tens of microseconds.
+    """
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
     for i in range(steps):
-        starts[i].record()
         fn(i)
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
-    each = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return starts[0].elapsed_time(ends[-1]), each
+    return start.elapsed_time(end)
+
+
+def _reps(fn: Callable[[int], None], floor: int, target_ms: float = 20.0) -> int:
+    """Calls that fill about `target_ms` of GPU time (at least `floor`), from a three-call estimate."""
+    est = _time_gpu(fn, 3, 1) / 3
+    return max(floor, min(2000, math.ceil(target_ms / max(est, 1e-3))))
 
 
 def _rate(work: float, ms: float, unit: str) -> float:
@@ -551,8 +560,8 @@ def _rate(work: float, ms: float, unit: str) -> float:
 
 
 def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
-    _, each = _time_gpu(wl.launch, steps, warmup)
-    avg = sum(each) / len(each)
+    """The dominant kernel's average launch: `steps` back-to-back launches between two events."""
+    avg = _time_gpu(wl.launch, steps, warmup) / steps
     achieved = _rate(wl.kernel_work, avg, wl.unit)
     hbm = wl.unit == "TB/s"
     peak = HBM_PEAK_TBS if hbm else BF16_PEAK_TFLOPS
@@ -596,7 +605,7 @@ def _torch_on_gpu(wl: Workload, ours_ms: float, steps: int, warmup: int) -> dict
     compares against."""
     if wl.torch_step is None:
         return None
-    total, _ = _time_gpu(wl.torch_step, steps, warmup)
+    total = _time_gpu(wl.torch_step, steps, warmup)
     per = total / steps
     return {"ms_per_step": round(per, 4), "value": round(_rate(wl.work, per, wl.unit), 4),
             "speedup": round(per / ours_ms, 3)}
@@ -627,7 +636,7 @@ def main(argv=None) -> int:
     print(f"bench: workload {args.workload}, {args.warmup} warmup + {args.steps} steps", file=sys.stderr, flush=True)
     wl = make_workload(args.workload, dev)
     torch.cuda.synchronize()
-    total_ms, _ = _time_gpu(wl.step, args.steps, args.warmup)
+    total_ms = _time_gpu(wl.step, args.steps, args.warmup)
     ms_per_step = total_ms / args.steps
     value = _rate(wl.work, ms_per_step, wl.unit)
     print(f"bench: {wl.name} {ms_per_step:.4f} ms/step, {value:.3f} {wl.unit}", file=sys.stderr, flush=True)
@@ -649,12 +658,13 @@ def main(argv=None) -> int:
                 continue
             torch.cuda.empty_cache()
             wl_o = make_workload(name, dev)
-            reps = max(5, args.steps // 2)
-            tot, _ = _time_gpu(wl_o.step, reps, 2)
+            reps = _reps(wl_o.step, max(5, args.steps // 2))
+            tot = _time_gpu(wl_o.step, reps, 2)
             per = tot / reps
-            entry = {"workload": wl_o.description, "ms_per_step": round(per, 4),
+            entry = {"workload": wl_o.description, "steps": reps, "ms_per_step": round(per, 4),
                      "value": round(_rate(wl_o.work, per, wl_o.unit), 4), "unit": wl_o.unit,
-                     "roofline": _roofline(wl_o, reps, 2), "torch_gpu": _torch_on_gpu(wl_o, per, reps, 2)}
+                     "roofline": _roofline(wl_o, _reps(wl_o.launch, reps), 2),
+                     "torch_gpu": _torch_on_gpu(wl_o, per, reps, 2)}
             if not args.no_cpu:
                 entry["cpu_baseline"] = _cpu_baseline(wl_o)
             others[name] = entry

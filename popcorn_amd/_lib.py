@@ -61,6 +61,8 @@ class KernelError(RuntimeError):
 def load(path: Path | str | None = None) -> ctypes.CDLL:
     """Load (once) and type the library; raises if it is missing or mismatched."""
     global _lib
+    if _lib is not None and path is None:  # the per-call path: no lock once loaded
+        return _lib
     with _lock:
         if _lib is not None and path is None:
             return _lib
@@ -90,8 +92,17 @@ def check(status: int, lib: ctypes.CDLL | None = None) -> None:
         raise KernelError(f"popcorn_amd: {message or f'status {status}'}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on `device`."""
+    """hipStream_t of torch's current stream on `device`.
+
+    torch's raw-stream query skips building a Stream object (about 2 us per
+    call); the public `current_stream` is the path where it is absent.
+    """
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

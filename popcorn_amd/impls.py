@@ -75,41 +75,49 @@ def _table_dtype(name: str, cos: Tensor, sin: Tensor) -> torch.dtype:
 # --------------------------------------------------------------------------- rms_norm
 
 
+def _rms_norm_fwd(x: Tensor, weight: Tensor, bias: Tensor | None, eps: float, want_rstd: bool):
+    """One pk_rmsnorm_fwd launch: (y in x's shape, x as [rows, cols], weight, rstd or None)."""
+    device = _require_cuda(x, weight, bias)
+    dtype, wdtype = _norm_dtypes("rms_norm", x, weight, bias)
+    cols = x.shape[-1]
+    if weight.shape != (cols,) or (bias is not None and bias.shape != (cols,)):
+        raise ValueError(f"popcorn_amd.rms_norm: weight/bias must be [{cols}]")
+    x2 = x.reshape(-1, cols)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    rows = x2.shape[0]
+    y = torch.empty(x.shape, dtype=wdtype, device=device)
+    rstd = torch.empty(rows, dtype=torch.float32, device=device) if want_rstd else None
+    lib = _lib.load()
+    _lib.check(
+        lib.pk_rmsnorm_fwd(
+            x2.data_ptr(),
+            w.data_ptr(),
+            None if b is None else b.data_ptr(),
+            y.data_ptr(),
+            None if rstd is None else rstd.data_ptr(),
+            rows,
+            cols,
+            float(eps),
+            _lib.DTYPE_CODES[dtype],
+            _lib.DTYPE_CODES[wdtype],
+            _lib.stream_handle(device),
+        ),
+        lib,
+    )
+    return y, x2, w, rstd
+
+
 class _RMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, eps: float) -> Tensor:
-        device = _require_cuda(x, weight, bias)
-        dtype, wdtype = _norm_dtypes("rms_norm", x, weight, bias)
-        cols = x.shape[-1]
-        if weight.shape != (cols,) or (bias is not None and bias.shape != (cols,)):
-            raise ValueError(f"popcorn_amd.rms_norm: weight/bias must be [{cols}]")
-        x2 = x.reshape(-1, cols).contiguous()
-        w = weight.contiguous()
-        b = bias.contiguous() if bias is not None else None
-        rows = x2.shape[0]
-        y = torch.empty(x2.shape, dtype=wdtype, device=device)
-        rstd = torch.empty(rows, dtype=torch.float32, device=device)
-        lib = _lib.load()
-        _lib.check(
-            lib.pk_rmsnorm_fwd(
-                x2.data_ptr(),
-                w.data_ptr(),
-                b.data_ptr() if b is not None else None,
-                y.data_ptr(),
-                rstd.data_ptr(),
-                rows,
-                cols,
-                float(eps),
-                _lib.dtype_code(dtype),
-                _lib.dtype_code(wdtype),
-                _lib.stream_handle(device),
-            ),
-            lib,
-        )
+        y, x2, w, rstd = _rms_norm_fwd(x, weight, bias, eps, want_rstd=True)
         ctx.save_for_backward(x2, w, rstd)
-        ctx.has_bias = b is not None
+        ctx.has_bias = bias is not None
         ctx.shape = x.shape
-        return y.view(x.shape)
+        return y
 
     @staticmethod
     def backward(ctx, dy: Tensor):
@@ -157,9 +165,13 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
     (fp32, bf16 or fp16), or a 16-bit x with fp32 weight and bias, where the
     normalized x is rounded to x's dtype and the output promotes to fp32
     (kernels/rms_norm.py:29). Backward gives dx (x's dtype), dweight, dbias
-    (the weight's).
+    (the weight's). Without a gradient to track, the call is one launch with no
+    autograd node and no saved statistics.
     """
-    return _RMSNorm.apply(x, weight, bias, eps)
+    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad
+                                    or (bias is not None and bias.requires_grad)):
+        return _RMSNorm.apply(x, weight, bias, eps)
+    return _rms_norm_fwd(x, weight, bias, eps, want_rstd=False)[0]
 
 
 # --------------------------------------------------------------------------- add_rms_norm
