@@ -7,7 +7,9 @@
 //               forward; keys streamed through LDS in tiles of 32. Per tile
 //               each wave recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //               P = exp2(s*c - lse2) from the forward's log-sum-exp and
-//               dS = P (dP - D), and accumulates dQ^T += K^T dS^T. Its prologue
+//               dS = P (dP - D), and accumulates dQ^T += K^T dS^T, with the
+//               dQ products of one tile interleaved with the S and dP
+//               products of the next (software-pipelined). Its prologue
 //               also computes D = rowsum(dO * O) for its rows and stores it,
 //               with lse2 = lse * log2(e), for the second kernel.
 //   dkdv kernel one block = 128 keys of one (sequence, kv head) in four
@@ -21,8 +23,12 @@
 //               forms dS = P (dP - D) and accumulates dK^T += Q^T dS. Splitting
 //               the roles halves each wave's registers (one fragment set, one
 //               accumulator), which is what lets two waves share each SIMD.
-//               Query tiles (with their lse2 and D rows) arrive two steps ahead
-//               through four LDS stages. A block walks its q heads' tiles one
+//               Each step is software-pipelined: a wave forms the factors of
+//               one tile from the score block it computed in the step before,
+//               then runs that tile's accumulation interleaved with the next
+//               tile's score block. Query tiles (with their lse2 and D rows)
+//               arrive through six LDS stages, two tiles in flight beyond the
+//               three a step reads. A block walks its q heads' tiles one
 //               after another, so when the grid is too small to fill the
 //               device the q heads of each group are split over several blocks
 //               that leave fp32 partials, and a third kernel adds them in
@@ -123,8 +129,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   constexpr int TI = BN * KCH / NT;  // direct loads per thread per tile of K (and of V): 2 or 1
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ks[2][BN * L::ST];
-  __shared__ __attribute__((aligned(16))) T Vs[2][BN * L::ST];
+  constexpr int NSQ = 4;  // K/V tile stages: the two tiles a step reads, one in flight, one landing
+  __shared__ __attribute__((aligned(16))) T Ks[NSQ][BN * L::ST];
+  __shared__ __attribute__((aligned(16))) T Vs[NSQ][BN * L::ST];
 
   // work item: (q tile, batch, kv head, head quad), longest causal rows
   // first; the waves are gp q heads of one kv group (gp = 4, 2 or 1, the
@@ -236,48 +243,63 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
-  issue(0, 0);
-  lds_loads_landed();
+  // Software-pipelined steps, as in the dk/dv kernel: step t forms dS of
+  // tile u = t - 1 from the S and dP blocks computed in step t - 1, then runs
+  // tile u's dQ products interleaved with the S and dP products of tile u + 1.
+  // Step t reads tiles t - 1 and t, issues tile t + NSQ - 2 into the stage of
+  // tile t - 2 (last read in step t - 1) and ends once tile t + 1 has landed.
+  // Tile indices are clamped into the range at the edges, where dS is zero.
+  // (Tiles wholly past a wave's rows are masked to zero, not skipped.)
+#pragma unroll
+  for (int j = 0; j < NSQ - 2; ++j) issue(min(j, n_tiles - 1), j);
+  lds_loads_landed();  // all of them: the dsum stores above share the counter
   __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    issue(min(t + 1, n_tiles - 1), buf ^ 1);  // its previous tile was last read in step t - 1
-    const int kv0 = t * BN;
-    if (!(CAUSAL && kv0 > wave_first + 31)) {
-      const T* ks = Ks[buf];
-      const T* vs = Vs[buf];
-      // 2 KK score products (S^T from K, dP^T from V, alternating), then DT x 2
-      // products of dQ^T; fragment reads run kRingDq products ahead, and
-      // sched_barrier keeps that order
-      constexpr int RING = kRingDq;
-      constexpr int NSC = 2 * KK, NALL = 3 * KK;
-      auto fetch = [&](int i) -> Frag {
-        if (i < NSC) return *reinterpret_cast<const Frag*>((i & 1 ? vs : ks) + a_lane[i / 2]);
-        const int u = i - NSC, c = u / DT, dt = u % DT;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[0][dt] + 16 * c * L::ST));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ks + t_lane[1][dt] + 16 * c * L::ST));
-        return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      };
-      static_assert(RING <= NSC && NSC + RING <= NALL, "ring reads stay inside the run");
-      Frag ring[RING];
+  // product 3h: dQ step h (A = K^T from transposing reads of the tile at ka:
+  // 16 keys c = h / DT, dims 32 (h % DT) ..; B = dsf[c]); 3h + 1: S^T step h
+  // (A = K fragment h of the tile at kn, B = Q^T); 3h + 2: dP^T step h (A = V
+  // fragment h of the tile at vn, B = dO^T). Reads run kRingDq products ahead.
+  constexpr int RING = kRingDq;
+  constexpr int NP = 3 * KK;
+  static_assert(RING <= NP, "the ring's first reads stay inside the run");
+  f32x16 s, dp;  // S^T and dP^T of the wave's next tile
+  auto run = [&](const T* ka, const Frag (&dsf)[2], const T* kn, const T* vn) {
+    auto fetch = [&](int i) -> Frag {
+      const int h = i / 3;
+      if (i % 3 == 1) return *reinterpret_cast<const Frag*>(kn + a_lane[h]);
+      if (i % 3 == 2) return *reinterpret_cast<const Frag*>(vn + a_lane[h]);
+      const int c = h / DT, dt = h % DT;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ka + t_lane[0][dt] + 16 * c * L::ST));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ka + t_lane[1][dt] + 16 * c * L::ST));
+      return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    Frag ring[RING];
 #pragma unroll
-      for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
-      f32x16 s, dp;
+    for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
 #pragma unroll
-      for (int i = 0; i < NSC; ++i) {
-        const Frag f = ring[i % RING];
-        ring[i % RING] = fetch(i + RING);
-        if (i & 1)
-          dp = Mma<T>::run(f, gf[i / 2], dp);
-        else
-          s = Mma<T>::run(f, qf[i / 2], s);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int i = 0; i < NP; ++i) {
+      const Frag f = ring[i % RING];
+      if (i + RING < NP) ring[i % RING] = fetch(i + RING);
+      const int h = i / 3;
+      if (i % 3 == 0)
+        acc[h % DT] = Mma<T>::run(f, dsf[h / DT], acc[h % DT]);
+      else if (i % 3 == 1)
+        s = Mma<T>::run(f, qf[h], s);
+      else
+        dp = Mma<T>::run(f, gf[h], dp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const int lim = CAUSAL ? min(q_row, S - 1) : S - 1;
+  for (int t = 0; t <= n_tiles; ++t) {
+    issue(min(t + NSQ - 2, n_tiles - 1), (t + NSQ - 2) % NSQ);
+    const int u = t - 1;
+    Frag dsf[2];
+    if (u >= 0) {
+      // dS = P (dP - D), P = exp2(s c - lse2); keys a row must not see get 0
+      const int kv0 = u * BN;
       const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > S;
-      const int lim = CAUSAL ? min(q_row, S - 1) : S - 1;
-      Frag dsf[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -287,20 +309,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
           if (need_mask) p = kv0 + 8 * (r >> 2) + 4 * g + (r & 3) <= lim ? p : 0.f;
           dsf[c][j] = (T)(p * (dp[r] - dsum));
         }
-      __builtin_amdgcn_sched_barrier(0);
-      // dQ^T += K^T dS^T: K^T fragments from transposing reads of the K tile
+    } else {
 #pragma unroll
-      for (int i = NSC; i < NALL; ++i) {
-        const Frag f = ring[i % RING];
-        if (i + RING < NALL) ring[i % RING] = fetch(i + RING);
-        const int u = i - NSC;
-        acc[u % DT] = Mma<T>::run(f, dsf[u / DT], acc[u % DT]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dsf[c][j] = (T)0.f;
     }
-    lds_loads_landed();
+    const int sa = max(u, 0) % NSQ, sn = min(u + 1, n_tiles - 1) % NSQ;
+    run(Ks[sa], dsf, Ks[sn], Vs[sn]);  // dQ^T += K^T dS^T; S^T, dP^T of the next tile
+    loads_landed_but<(NSQ - 3) * 2 * TI>();
     __syncthreads();
   }
+  lds_loads_landed();  // tiles issued past the end, before the block's LDS is released
 
   if (row_ok) {
     T* drow = static_cast<T*>(a.dq) + b * a.dqs[0] + hq * a.dqs[2] + (int64_t)(start + q_row) * a.dqs[1];
@@ -326,7 +346,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   constexpr int KCH = D / 8;             // 16-byte chunks per row
   constexpr int SLOTS = BQ * KCH;        // 16-byte slots of a Q (or dO) tile: 512 or 256
   constexpr int TI = 2 * SLOTS / NT2;    // direct loads per thread per tile (Q and dO together): 2 or 1
-  constexpr int NS = 4;                  // query tiles resident or in flight in LDS
+  constexpr int NS = 6;                  // query tiles resident or in flight in LDS
   constexpr int PER_ISSUE = TI + 1;      // loads each wave issues per tile (tiles, one row vector)
   constexpr int TILE = BQ * D;
   constexpr int KK = D / 16;
@@ -472,109 +492,125 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   };
   // P buffer layout: value r of lane l at (r / 8) * 512 + 8 * l + r % 8 (16-byte lane stride)
 
-  // Step t: role 0 takes tile t (P into Pb[t & 1]), role 1 tile t - 1 (P from
-  // Pb[(t - 1) & 1]). Tile t + NS - 2 is issued into the stage of tile t - 2,
-  // which role 1 finished in step t - 1; the step ends once tile t + 1 has landed.
+  // Software-pipelined steps. In step t a wave works on tile u = t - 1 - role
+  // (role 1 trails role 0 by one tile, whose P it reads from LDS): it turns
+  // the score block of tile u, computed in the previous step, into the B
+  // fragments of its accumulation (role 0: P, also left in Pb[u & 1] as fp16;
+  // role 1: dS = P (dP - D)), then runs one interleaved set of products:
+  // tile u's accumulation and tile u + 1's score block. The products never
+  // wait on each other's results within a step, and the vector work of one
+  // wave overlaps the products of the other wave on its SIMD.
+  //
+  // Step t reads tiles t - 2 .. t (the stage ring holds NS). It issues tile
+  // t + NS - 3 into the stage of tile t - 3, last read in step t - 1, and
+  // ends once tile t + 1 has landed, leaving NS - 4 tiles in flight. Before
+  // the first tile and after the last the wave's tile indices are clamped into
+  // the range (those stages hold landed, finite data) and its accumulation
+  // factors are zero, so the edge steps run the same products to no effect.
+  static_assert(NS >= 5, "the step reads three resident tiles and keeps at least one in flight");
 #pragma unroll
-  for (int j = 0; j < NS - 2; ++j) issue(j);
-  loads_landed_but<(NS - 3) * PER_ISSUE>();
+  for (int j = 0; j < NS - 3; ++j) issue(j);
+  loads_landed_but<(NS - 4) * PER_ISSUE>();
   __syncthreads();
-  // One step's 16 products: 8 of the score block (A from the tile at `pbase`,
-  // B = the lane's key row) then 8 of the accumulation (A^T from transposing
-  // reads of the tile at `abase`, B from `mid`, which turns the score block
-  // into the B fragments between the two halves). Fragment reads run
-  // kRingDkdv products ahead, across the two halves.
+  // The step's products: product 2h is accumulation h (A^T from transposing
+  // reads of the tile at abase: 16 keys c = h / DT, dims 32 (h % DT) ..; B =
+  // mf[c]), product 2h + 1 is score step h (A from the tile at pbase, B = the
+  // lane's key row) into sres. Fragment reads run kRingDkdv products ahead.
   constexpr int RING = kRingDkdv;
-  auto run16 = [&](const T* pbase, const T* abase, auto mid) {
+  constexpr int NP = 2 * KK;
+  static_assert(RING <= NP, "the ring's first reads stay inside the run");
+  f32x16 sres;  // score block of the wave's next tile
+  auto run = [&](const T* abase, const Frag (&mf)[2], const T* pbase) {
     auto fetch = [&](int i) -> Frag {
-      if (i < KK) return *reinterpret_cast<const Frag*>(pbase + a_lane[i]);
-      const int u = i - KK, c = u / DT, dt = u % DT;
+      const int h = i >> 1;
+      if (i & 1) return *reinterpret_cast<const Frag*>(pbase + a_lane[h]);
+      const int c = h / DT, dt = h % DT;
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[0][dt] + 16 * c * L::ST));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[1][dt] + 16 * c * L::ST));
       return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    static_assert(RING <= 2 * KK, "the ring's first reads stay inside the run");
     Frag ring[RING];
 #pragma unroll
     for (int i = 0; i < RING; ++i) ring[i] = fetch(i);
-    f32x16 sres;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sres[r] = 0.f;
 #pragma unroll
-    for (int i = 0; i < KK; ++i) {
+    for (int i = 0; i < NP; ++i) {
       const Frag f = ring[i % RING];
-      if (i + RING < 2 * KK) ring[i % RING] = fetch(i + RING);  // at head_dim 64 the run is only 8 long
-      sres = Mma<T>::run(f, bf[i], sres);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    Frag bfr[2];
-    mid(sres, bfr);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = KK; i < 2 * KK; ++i) {
-      const Frag f = ring[i % RING];
-      if (i + RING < 2 * KK) ring[i % RING] = fetch(i + RING);
-      const int u = i - KK;
-      acc[u % DT] = Mma<T>::run(f, bfr[u / DT], acc[u % DT]);
+      if (i + RING < NP) ring[i % RING] = fetch(i + RING);
+      const int h = i >> 1;
+      if (i & 1)
+        sres = Mma<T>::run(f, bf[h], sres);
+      else
+        acc[h % DT] = Mma<T>::run(f, mf[h / DT], acc[h % DT]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  for (int t = 0; t <= n_it; ++t) {
-    issue((t + NS - 2) % NS);
-    if (role == 0) {
-      if (t < n_it) {
-        const int st = t % NS;
-        const T* qs = QG[st];
-        const int q0 = (u0 + t % n_u) * BQ;
-        float l2[16];
-        rows16(RV[st][0], l2);
-        // tiles wholly before this slice's keys (causal) are masked to zero, not skipped
-        const bool need_mask = (CAUSAL && q0 < kw0 + 32) || !key_ok || q0 + BQ > S;
-        _Float16* pw = Pb[t & 1][slice];
-        run16(qs, qs + TILE, [&](const f32x16& s, Frag (&pf)[2]) {
-          float p[16];
+  for (int t = 0; t <= n_it + 1; ++t) {
+    issue((t + NS - 3) % NS);
+    const int u = t - 1 - role;
+    const bool live = u >= 0 && u < n_it;
+    Frag mf[2];
+    if (live) {
+      const int st = u % NS;
+      float rv[16];  // the tile rows' lse2 (role 0) or D (role 1)
+      rows16(RV[st][role], rv);
+      if (role == 0) {
+        // P = exp2(s c - lse2); keys a row must not see, and rows or keys past
+        // the end, get 0. The test for a mask is wave-uniform (the slice's
+        // keys, not the lane's), so the unmasked steps branch past it.
+        const int q0 = (u0 + u % n_u) * BQ;
+        const bool need_mask = (CAUSAL && q0 < kw0 + 32) || kw0 + 32 > S || q0 + BQ > S;
+        float p[16];
+        if (need_mask) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], cs, -l2[r]));
-            if (need_mask) {
-              const int qrow = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
-              p[r] = key_ok && qrow < S && (!CAUSAL || key <= qrow) ? p[r] : 0.f;
-            }
+            const int qrow = q0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            const bool ok = key_ok & (qrow < S) & (!CAUSAL | (key <= qrow));
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sres[r], cs, -rv[r]));
+            p[r] = ok ? e : 0.f;
           }
+        } else {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            h8 hv;
+          for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sres[r], cs, -rv[r]));
+        }
+        _Float16* pw = Pb[u & 1][slice];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) hv[i] = (_Float16)p[8 * j + i];
-            *reinterpret_cast<h8*>(pw + 512 * j + 8 * lane) = hv;
-          }
+        for (int j = 0; j < 2; ++j) {
+          h8 hv;
 #pragma unroll
-          for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pf[c][j] = (T)p[8 * c + j];
-        });  // dV^T += dO^T P
-      }
-    } else if (t > 0) {
-      const int u = t - 1;
-      const int st = u % NS;
-      const T* qs = QG[st];
-      float dd[16], p[16];
-      rows16(RV[st][1], dd);
-      const _Float16* pr = Pb[u & 1][slice];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const h8 x = *reinterpret_cast<const h8*>(pr + 512 * j + 8 * lane);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[8 * j + i] = (float)x[i];
-      }
-      run16(qs + TILE, qs, [&](const f32x16& dp, Frag (&dsf)[2]) {
+          for (int i = 0; i < 8; ++i) hv[i] = (_Float16)p[8 * j + i];
+          *reinterpret_cast<h8*>(pw + 512 * j + 8 * lane) = hv;
+        }
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) dsf[c][j] = (T)(p[8 * c + j] * (dp[8 * c + j] - dd[8 * c + j]));
-      });  // dK^T += Q^T dS
+          for (int j = 0; j < 8; ++j) mf[c][j] = (T)p[8 * c + j];
+      } else {
+        // dS = P (dP - D), with the P role 0 left for this tile one step ago
+        const _Float16* pr = Pb[u & 1][slice];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const h8 x = *reinterpret_cast<const h8*>(pr + 512 * j + 8 * lane);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int r = 8 * j + i;
+            mf[j][i] = (T)((float)x[i] * (sres[r] - rv[r]));
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mf[c][j] = (T)0.f;
     }
-    loads_landed_but<(NS - 3) * PER_ISSUE>();
+    // role 0: dV^T += dO^T P and S = Q K^T of the next tile;
+    // role 1: dK^T += Q^T dS and dP = dO V^T of the next tile
+    const T* ta = QG[min(max(u, 0), n_it - 1) % NS];
+    const T* ts = QG[min(max(u + 1, 0), n_it - 1) % NS];
+    run(role == 0 ? ta + TILE : ta, mf, role == 0 ? ts : ts + TILE);
+    loads_landed_but<(NS - 4) * PER_ISSUE>();
     __syncthreads();
   }
   loads_landed_but<0>();  // tiles issued past the end, before the block's LDS is released
