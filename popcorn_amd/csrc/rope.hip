@@ -249,18 +249,21 @@ struct NormArgs {
   int batch, seq, half, cos_batch;
   int chunks, shift;  // chunks per row (a power of two) and its log2
   int rows, tiles;    // positions per block tile, tiles per batch row
-  int group;          // heads per block
+  int group[2];       // heads per block of q and of k
   int groups_q;       // head groups of q; groups [groups_q, groups_q + groups_k) are k's
   float eps, inv_d;
   float* part;        // backward: [blocks, 2 * head_dim] partial dw rows
 };
 
 struct NormPlan {
-  int rows, tiles, group, groups_q, groups_k;
+  int rows, tiles, group[2], groups_q, groups_k;
   int64_t blocks;
 };
 
-// Head groups sized for about eight 256-thread blocks per CU, as rope_kernel.
+// Head groups sized for about eight 256-thread blocks per CU, as rope_kernel,
+// then evened out on each side: a side of n heads in g groups takes groups of
+// ceil(n / g), so no block carries a short remainder (32 q heads in groups of
+// at most 10 become four groups of 8, not 10, 10, 10 and 2).
 NormPlan norm_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int chunks) {
   NormPlan p{};
   p.rows = kThreads / chunks;
@@ -270,9 +273,15 @@ NormPlan norm_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq
   if (all == 0 || tiles == 0) return p;
   int64_t groups = (8 * (int64_t)cu_count() + tiles - 1) / tiles;
   groups = groups < 1 ? 1 : (groups > all ? all : groups);
-  p.group = (int)((all + groups - 1) / groups);
-  p.groups_q = (int)((q_heads + p.group - 1) / p.group);
-  p.groups_k = (int)((kv_heads + p.group - 1) / p.group);
+  const int64_t most = (all + groups - 1) / groups;  // heads per block at most
+  const int64_t heads[2] = {q_heads, kv_heads};
+  int n[2];
+  for (int t = 0; t < 2; ++t) {
+    n[t] = (int)((heads[t] + most - 1) / most);
+    p.group[t] = n[t] > 0 ? (int)((heads[t] + n[t] - 1) / n[t]) : 1;
+  }
+  p.groups_q = n[0];
+  p.groups_k = n[1];
   p.blocks = tiles * (p.groups_q + p.groups_k);
   return p;
 }
@@ -296,8 +305,8 @@ __device__ __forceinline__ NormBlock norm_block(const NormArgs& a) {
   int gi = (int)(blk / (unsigned)a.batch);
   nb.t = gi >= a.groups_q;
   if (nb.t) gi -= a.groups_q;
-  nb.h_begin = gi * a.group;
-  nb.h_end = nb.h_begin + a.group < a.heads[nb.t] ? nb.h_begin + a.group : a.heads[nb.t];
+  nb.h_begin = gi * a.group[nb.t];
+  nb.h_end = nb.h_begin + a.group[nb.t] < a.heads[nb.t] ? nb.h_begin + a.group[nb.t] : a.heads[nb.t];
   nb.s = tile * a.rows + (int)(threadIdx.x >> a.shift);
   nb.j = (int)(threadIdx.x & (a.chunks - 1));
   return nb;
@@ -530,7 +539,8 @@ int norm_setup(const char* who, NormArgs& a, NormPlan& p, const void* q, const v
   a.cos_batch = (int)cos_batch;
   a.rows = p.rows;
   a.tiles = p.tiles;
-  a.group = p.group;
+  a.group[0] = p.group[0];
+  a.group[1] = p.group[1];
   a.groups_q = p.groups_q;
   a.inv_d = head_dim > 0 ? 1.0f / (float)head_dim : 0.f;
   if (p.blocks == 0) return PK_OK;  // nothing to read (a backward still zeroes dw)
