@@ -22,7 +22,9 @@
 //               holds V, computes dP = dO V^T one step later, reads that P,
 //               forms dS = P (dP - D) and accumulates dK^T += Q^T dS. Splitting
 //               the roles halves each wave's registers (one fragment set, one
-//               accumulator), which is what lets two waves share each SIMD.
+//               accumulator), which is what lets two waves share each SIMD
+//               (four at head_dim 64, whose kernel fits 128 registers, so
+//               two blocks share a CU).
 //               Each step is software-pipelined: a wave forms the factors of
 //               one tile from the score block it computed in the step before,
 //               then runs that tile's accumulation interleaved with the next
@@ -338,8 +340,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 constexpr int NT2 = 512;  // dkdv kernel: 8 waves, two per SIMD
 
+// head_dim 64 fits 128 registers, so two blocks share a CU (four waves per SIMD)
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(2))) void attn_bwd_dkdv_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void attn_bwd_dkdv_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
