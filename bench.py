@@ -71,10 +71,13 @@ class Workload:
     step: Callable[[int], None]  # step(i): one pass of the drop-in call on input copy i
     kernel: str  # dominant kernel's name (as rocprofv3 reports it, prefix)
     kernel_work: float  # algorithmic bytes / FLOPs of one launch of that kernel
-    launch: Callable[[int], None]  # one launch of the dominant kernel alone on input copy i
+    launch: Callable[[int], None]  # one call of the C entry point that runs the dominant kernel, on input copy i
     config: dict = field(default_factory=dict)
     cpu: Callable[[], tuple[float, str]] | None = None  # -> (throughput in unit, sample description)
     torch_step: Callable[[int], None] | None = None  # Popcorn's torch reference on the GPU, same inputs
+    # every kernel one `launch` runs, when it is more than the dominant one (the launch's time then
+    # covers them all, so the achieved rate of the dominant kernel is understated, never overstated)
+    launch_kernels: tuple[str, ...] = ()
 
 
 def _copies(nbytes: int) -> int:
@@ -302,7 +305,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                         "weights [128], bf16 cos/sin [1,4096,128]", "bf16", "TB/s", fwd_bytes + bwd_bytes, step,
                         "qk_norm_rope_bwd_kernel", bwd_bytes, launch,
                         {"batch": B, "q_heads": HQ, "kv_heads": HKV, "seq": S, "head_dim": D, "cos_batch": 1,
-                         "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step)
+                         "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step,
+                        launch_kernels=("qk_norm_rope_bwd_kernel", "column_sum_stage", "column_sum_final"))
 
     if name == "c4":
         rows, cols = 65536, 8192
@@ -351,7 +355,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
 
         return Workload("c4", "RMSNorm fwd+bwd bf16 x, dy [65536, 8192]", "bf16", "TB/s", fwd_bytes + bwd_bytes,
                         step, "rmsnorm_bwd_vec", bwd_bytes, launch,
-                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step)
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "dtype": "bf16"}, cpu, torch_step,
+                        launch_kernels=("rmsnorm_bwd_vec", "column_sum_stage", "column_sum_final"))
 
     if name == "add_rmsnorm":
         # not a BASELINE config: the next op on the norm path (residual add + RMSNorm) at C4's shape
@@ -401,7 +406,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
 
         return Workload("add_rmsnorm", "add_rms_norm fwd+bwd bf16 x, residual, dy, ds [65536, 8192], offset 1",
                         "bf16", "TB/s", fwd_bytes + bwd_bytes, step, "rmsnorm_bwd_vec", bwd_bytes, launch,
-                        {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu, torch_step)
+                        {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu, torch_step,
+                        launch_kernels=("rmsnorm_bwd_vec", "column_sum_stage", "column_sum_final"))
 
     if name == "attn_bwd":
         # not a BASELINE config: attention forward + backward at C5's shape (bf16, causal)
@@ -449,7 +455,8 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         return Workload("attn_bwd", "Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16",
                         "TFLOP/s", fwd_flops + bwd_flops, step, "attn_bwd", bwd_flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
-                         "dtype": "bf16"}, cpu, torch_step)
+                         "dtype": "bf16"}, cpu, torch_step,
+                        launch_kernels=("attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"))
 
     if name == "c5":
         B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
@@ -560,7 +567,11 @@ def _rate(work: float, ms: float, unit: str) -> float:
 
 
 def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
-    """The dominant kernel's average launch: `steps` back-to-back launches between two events."""
+    """The dominant kernel's average launch: `steps` back-to-back launches between two events.
+
+    A launch is one call of the C entry point; where that runs more kernels than the dominant one
+    (`launch_covers`), their time is charged to it too.
+    """
     avg = _time_gpu(wl.launch, steps, warmup) / steps
     achieved = _rate(wl.kernel_work, avg, wl.unit)
     hbm = wl.unit == "TB/s"
@@ -575,6 +586,7 @@ def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
         "avg_launch_us": round(avg * 1e3, 2),
         "work_per_launch": wl.kernel_work,
         "traffic": MEASURED_TRAFFIC.get(wl.name),
+        **({"launch_covers": list(wl.launch_kernels)} if wl.launch_kernels else {}),
     }
 
 
