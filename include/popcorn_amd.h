@@ -6,7 +6,9 @@
  *   - every pointer is a device pointer owned by the caller (torch);
  *   - sizes and strides are int64, strides count elements, the last dimension
  *     is always contiguous;
- *   - `stream` is a hipStream_t; work is enqueued there and nothing synchronises;
+ *   - `stream` is a hipStream_t of the current HIP device (NULL: that device's
+ *     null stream), and the pointers are memory of that device; work is
+ *     enqueued there and nothing synchronises;
  *   - the return value is a PK_* status; on anything but PK_OK the reason is in
  *     pk_last_error() (a per-thread string). No entry point falls back to
  *     another implementation: an unsupported call is an error.

@@ -6,6 +6,7 @@ missing or stale library raises, there is no fallback path.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import threading
 from pathlib import Path
@@ -104,6 +105,24 @@ def stream_handle(device: torch.device) -> int:
     if _raw_stream is not None and device.index is not None:
         return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def on_device(device: torch.device):
+    """A context in which `device` is the current HIP device: a no-op when it already is.
+
+    Kernels launch on the current device, and stream handle 0 (torch's default
+    stream) names that device's null stream, so a call whose tensors live on
+    another device makes theirs current around the launch and restores the
+    caller's afterwards, as torch's own operators do.
+    """
+    index = device.index
+    if index is None or index == (_get_device() if _get_device is not None else torch.cuda.current_device()):
+        return _NO_SWITCH
+    return torch.cuda.device(index)
 
 
 def dtype_code(dtype: torch.dtype) -> int:

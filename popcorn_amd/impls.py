@@ -91,22 +91,23 @@ def _rms_norm_fwd(x: Tensor, weight: Tensor, bias: Tensor | None, eps: float, wa
     y = torch.empty(x.shape, dtype=wdtype, device=device)
     rstd = torch.empty(rows, dtype=torch.float32, device=device) if want_rstd else None
     lib = _lib.load()
-    _lib.check(
-        lib.pk_rmsnorm_fwd(
-            x2.data_ptr(),
-            w.data_ptr(),
-            None if b is None else b.data_ptr(),
-            y.data_ptr(),
-            None if rstd is None else rstd.data_ptr(),
-            rows,
-            cols,
-            float(eps),
-            _lib.DTYPE_CODES[dtype],
-            _lib.DTYPE_CODES[wdtype],
-            _lib.stream_handle(device),
-        ),
-        lib,
-    )
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_rmsnorm_fwd(
+                x2.data_ptr(),
+                w.data_ptr(),
+                None if b is None else b.data_ptr(),
+                y.data_ptr(),
+                None if rstd is None else rstd.data_ptr(),
+                rows,
+                cols,
+                float(eps),
+                _lib.DTYPE_CODES[dtype],
+                _lib.DTYPE_CODES[wdtype],
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
     return y, x2, w, rstd
 
 
@@ -136,25 +137,26 @@ class _RMSNorm(torch.autograd.Function):
             code = _lib.dtype_code(x2.dtype)
             nbytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, code)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
-            _lib.check(
-                lib.pk_rmsnorm_bwd(
-                    x2.data_ptr(),
-                    w.data_ptr(),
-                    rstd.data_ptr(),
-                    dy2.data_ptr(),
-                    dx.data_ptr(),
-                    dw.data_ptr(),
-                    db.data_ptr() if db is not None else None,
-                    workspace.data_ptr(),
-                    nbytes,
-                    rows,
-                    cols,
-                    code,
-                    _lib.dtype_code(w.dtype),
-                    _lib.stream_handle(x2.device),
-                ),
-                lib,
-            )
+            with _lib.on_device(x2.device):
+                _lib.check(
+                    lib.pk_rmsnorm_bwd(
+                        x2.data_ptr(),
+                        w.data_ptr(),
+                        rstd.data_ptr(),
+                        dy2.data_ptr(),
+                        dx.data_ptr(),
+                        dw.data_ptr(),
+                        db.data_ptr() if db is not None else None,
+                        workspace.data_ptr(),
+                        nbytes,
+                        rows,
+                        cols,
+                        code,
+                        _lib.dtype_code(w.dtype),
+                        _lib.stream_handle(x2.device),
+                    ),
+                    lib,
+                )
         return dx.view(ctx.shape), dw, db, None
 
 
@@ -195,13 +197,14 @@ class _AddRMSNorm(torch.autograd.Function):
         s = torch.empty_like(x2)
         rstd = torch.empty(rows, dtype=torch.float32, device=device)
         lib = _lib.load()
-        _lib.check(
-            lib.pk_add_rmsnorm_fwd(
-                x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
-                float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
-            ),
-            lib,
-        )
+        with _lib.on_device(device):
+            _lib.check(
+                lib.pk_add_rmsnorm_fwd(
+                    x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
+                    float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
+                ),
+                lib,
+            )
         ctx.save_for_backward(s, w, rstd)
         ctx.offset = float(offset)
         ctx.shape = x.shape
@@ -226,14 +229,15 @@ class _AddRMSNorm(torch.autograd.Function):
             code = _lib.dtype_code(s.dtype)
             nbytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, code)
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=s.device)
-            _lib.check(
-                lib.pk_add_rmsnorm_bwd(
-                    s.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(),
-                    ds2.data_ptr() if ds2 is not None else None, dsum.data_ptr(), dw.data_ptr(),
-                    workspace.data_ptr(), nbytes, rows, cols, ctx.offset, code, _lib.stream_handle(s.device),
-                ),
-                lib,
-            )
+            with _lib.on_device(s.device):
+                _lib.check(
+                    lib.pk_add_rmsnorm_bwd(
+                        s.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(),
+                        ds2.data_ptr() if ds2 is not None else None, dsum.data_ptr(), dw.data_ptr(),
+                        workspace.data_ptr(), nbytes, rows, cols, ctx.offset, code, _lib.stream_handle(s.device),
+                    ),
+                    lib,
+                )
         # s = x + residual: both receive the gradient of s (as torch's add backward hands them)
         return dsum.view(ctx.shape), dsum.view(ctx.shape), dw, None, None
 
@@ -261,13 +265,14 @@ class _SwiGLU(torch.autograd.Function):
         a_c, b_c = a.contiguous(), b.contiguous()
         y = torch.empty_like(a_c)
         lib = _lib.load()
-        _lib.check(
-            lib.pk_swiglu_fwd(
-                a_c.data_ptr(), b_c.data_ptr(), y.data_ptr(), a_c.numel(), _lib.dtype_code(dtype),
-                _lib.stream_handle(device),
-            ),
-            lib,
-        )
+        with _lib.on_device(device):
+            _lib.check(
+                lib.pk_swiglu_fwd(
+                    a_c.data_ptr(), b_c.data_ptr(), y.data_ptr(), a_c.numel(), _lib.dtype_code(dtype),
+                    _lib.stream_handle(device),
+                ),
+                lib,
+            )
         ctx.save_for_backward(a_c, b_c)
         return y
 
@@ -277,13 +282,14 @@ class _SwiGLU(torch.autograd.Function):
         g = dy.to(a_c.dtype).contiguous()
         da, db = torch.empty_like(a_c), torch.empty_like(b_c)
         lib = _lib.load()
-        _lib.check(
-            lib.pk_swiglu_bwd(
-                g.data_ptr(), a_c.data_ptr(), b_c.data_ptr(), da.data_ptr(), db.data_ptr(), a_c.numel(),
-                _lib.dtype_code(a_c.dtype), _lib.stream_handle(a_c.device),
-            ),
-            lib,
-        )
+        with _lib.on_device(a_c.device):
+            _lib.check(
+                lib.pk_swiglu_bwd(
+                    g.data_ptr(), a_c.data_ptr(), b_c.data_ptr(), da.data_ptr(), db.data_ptr(), a_c.numel(),
+                    _lib.dtype_code(a_c.dtype), _lib.stream_handle(a_c.device),
+                ),
+                lib,
+            )
         return da, db
 
 
@@ -309,26 +315,27 @@ def _rotate(x: Tensor, cos: Tensor, sin: Tensor, out: Tensor, interleaved: bool,
         raise ValueError(f"popcorn_amd.rotary_embedding: half={half} > head_dim/2")
     lib = _lib.load()
     strides = (_lib._i64 * 6)(x.stride(0), x.stride(1), x.stride(2), out.stride(0), out.stride(1), out.stride(2))
-    _lib.check(
-        lib.pk_rotary(
-            x.data_ptr(),
-            cos.data_ptr(),
-            sin.data_ptr(),
-            out.data_ptr(),
-            strides,
-            batch,
-            seq,
-            heads,
-            head_dim,
-            half,
-            _lib.dtype_code(x.dtype),
-            _lib.dtype_code(cos.dtype),
-            int(interleaved),
-            int(conjugate),
-            _lib.stream_handle(device),
-        ),
-        lib,
-    )
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_rotary(
+                x.data_ptr(),
+                cos.data_ptr(),
+                sin.data_ptr(),
+                out.data_ptr(),
+                strides,
+                batch,
+                seq,
+                heads,
+                head_dim,
+                half,
+                _lib.dtype_code(x.dtype),
+                _lib.dtype_code(cos.dtype),
+                int(interleaved),
+                int(conjugate),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
 
 
 def _last_contiguous(t: Tensor) -> Tensor:
@@ -405,15 +412,16 @@ def _rope(q: Tensor | None, k: Tensor | None, cos: Tensor, sin: Tensor, transpos
     lib = _lib.load()
     st = (_lib._i64 * 12)(*strides(xq), *strides(xk), *strides(yq), *strides(yk))
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    _lib.check(
-        lib.pk_rope(
-            ptr(xq), ptr(xk), cs.data_ptr(), sn.data_ptr(), ptr(yq), ptr(yk), st, batch,
-            0 if q is None else q.shape[1], 0 if k is None else k.shape[1], seq, head_dim, cos.shape[0],
-            _lib.dtype_code(dtype), _lib.dtype_code(out_dtype), _lib.dtype_code(cs_dtype), int(transpose),
-            _lib.stream_handle(device),
-        ),
-        lib,
-    )
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_rope(
+                ptr(xq), ptr(xk), cs.data_ptr(), sn.data_ptr(), ptr(yq), ptr(yk), st, batch,
+                0 if q is None else q.shape[1], 0 if k is None else k.shape[1], seq, head_dim, cos.shape[0],
+                _lib.dtype_code(dtype), _lib.dtype_code(out_dtype), _lib.dtype_code(cs_dtype), int(transpose),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
     return yq, yk
 
 
@@ -461,7 +469,8 @@ def _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin):
     if q_weight.shape != (head_dim,) or k_weight.shape != (head_dim,):
         raise ValueError(f"popcorn_amd.qk_norm_rope: weights must be [{head_dim}]")
     if cos.shape[1:] != (seq, head_dim) or cos.shape[0] not in (1, batch):
-        raise ValueError(f"popcorn_amd.qk_norm_rope: cos/sin {tuple(cos.shape)} must be [1 or {batch}, {seq}, {head_dim}]")
+        raise ValueError(
+            f"popcorn_amd.qk_norm_rope: cos/sin {tuple(cos.shape)} must be [1 or {batch}, {seq}, {head_dim}]")
     return device, dtype, batch, seq, head_dim
 
 
@@ -485,15 +494,16 @@ class _QkNormRope(torch.autograd.Function):
         lib = _lib.load()
         st = (_lib._i64 * 12)(*(x for t in (q_, k_, yq, yk) for x in t.stride()[:3]))
         code = _lib.dtype_code(dtype)
-        _lib.check(
-            lib.pk_qk_norm_rope_fwd(
-                q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
-                yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
-                head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
-                _lib.stream_handle(device),
-            ),
-            lib,
-        )
+        with _lib.on_device(device):
+            _lib.check(
+                lib.pk_qk_norm_rope_fwd(
+                    q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
+                    yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
+                    head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
+                    _lib.stream_handle(device),
+                ),
+                lib,
+            )
         ctx.save_for_backward(q_, k_, qw, kw, cs, sn, rq, rk)
         ctx.out_dtype = out_dtype
         return yq, yk
@@ -515,15 +525,16 @@ class _QkNormRope(torch.autograd.Function):
             raise ValueError(f"popcorn_amd.qk_norm_rope: head_dim={head_dim} is not supported")
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q_.device)
         st = (_lib._i64 * 18)(*(x for t in (q_, k_, gq, gk, dq, dk) for x in t.stride()[:3]))
-        _lib.check(
-            lib.pk_qk_norm_rope_bwd(
-                q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
-                rq.data_ptr(), rk.data_ptr(), gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
-                dw.data_ptr(), ws.data_ptr(), nbytes, st, batch, q_.shape[1], k_.shape[1], seq, head_dim,
-                cs.shape[0], code, _lib.dtype_code(gdt), _lib.dtype_code(cs.dtype), _lib.stream_handle(q_.device),
-            ),
-            lib,
-        )
+        with _lib.on_device(q_.device):
+            _lib.check(
+                lib.pk_qk_norm_rope_bwd(
+                    q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
+                    rq.data_ptr(), rk.data_ptr(), gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                    dw.data_ptr(), ws.data_ptr(), nbytes, st, batch, q_.shape[1], k_.shape[1], seq, head_dim,
+                    cs.shape[0], code, _lib.dtype_code(gdt), _lib.dtype_code(cs.dtype), _lib.stream_handle(q_.device),
+                ),
+                lib,
+            )
         return dq, dk, dw[0], dw[1], None, None, None
 
 
@@ -582,14 +593,15 @@ def _attn_fwd(q, k, v, causal, softmax_scale, want_lse):
     lse = torch.empty((batch, q_heads, seq), dtype=torch.float32, device=device) if want_lse else None
     lib = _lib.load()
     strides = (_lib._i64 * 12)(*(s for t in (q_, k_, v_, o) for s in t.stride()[:3]))
-    _lib.check(
-        lib.pk_attn_fwd(
-            q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
-            strides, batch, seq, q_heads, kv_heads, head_dim, _scale(head_dim, softmax_scale), int(bool(causal)),
-            _lib.dtype_code(dtype), _lib.stream_handle(device),
-        ),
-        lib,
-    )
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_attn_fwd(
+                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
+                strides, batch, seq, q_heads, kv_heads, head_dim, _scale(head_dim, softmax_scale), int(bool(causal)),
+                _lib.dtype_code(dtype), _lib.stream_handle(device),
+            ),
+            lib,
+        )
     return o, lse
 
 
@@ -615,15 +627,16 @@ class _Attention(torch.autograd.Function):
             raise _lib.KernelError(f"pk_attn_bwd_workspace: invalid shape {tuple(q.shape)} / {tuple(k.shape)}")
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         strides = (_lib._i64 * 24)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:3]))
-        _lib.check(
-            lib.pk_attn_bwd(
-                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
-                ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), strides, batch, seq, q_heads,
-                k.shape[2], head_dim, _scale(head_dim, ctx.softmax_scale), int(ctx.causal), _lib.dtype_code(q.dtype),
-                _lib.stream_handle(q.device),
-            ),
-            lib,
-        )
+        with _lib.on_device(q.device):
+            _lib.check(
+                lib.pk_attn_bwd(
+                    q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
+                    ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), strides, batch, seq,
+                    q_heads, k.shape[2], head_dim, _scale(head_dim, ctx.softmax_scale), int(ctx.causal),
+                    _lib.dtype_code(q.dtype), _lib.stream_handle(q.device),
+                ),
+                lib,
+            )
         return dq, dk, dv, None, None
 
 
@@ -684,14 +697,15 @@ def _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want
     lse = torch.empty((q_heads, total), dtype=torch.float32, device=device) if want_lse else None
     lib = _lib.load()
     strides = (_lib._i64 * 8)(*(s for t in (q_, k_, v_, o) for s in t.stride()[:2]))
-    _lib.check(
-        lib.pk_attn_varlen_fwd(
-            q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
-            cu.data_ptr(), strides, num_seqs, total, longest, q_heads, k.shape[1], head_dim,
-            _scale(head_dim, softmax_scale), int(bool(causal)), _lib.dtype_code(dtype), _lib.stream_handle(device),
-        ),
-        lib,
-    )
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_attn_varlen_fwd(
+                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), lse.data_ptr() if lse is not None else None,
+                cu.data_ptr(), strides, num_seqs, total, longest, q_heads, k.shape[1], head_dim,
+                _scale(head_dim, softmax_scale), int(bool(causal)), _lib.dtype_code(dtype), _lib.stream_handle(device),
+            ),
+            lib,
+        )
     return o, lse
 
 
@@ -718,13 +732,14 @@ class _AttentionVarlen(torch.autograd.Function):
             raise _lib.KernelError(f"pk_attn_varlen_bwd_workspace: invalid shape {tuple(q.shape)} / {tuple(k.shape)}")
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
         strides = (_lib._i64 * 16)(*(s for t in (q_, k_, v_, o, do_, dq, dk, dv) for s in t.stride()[:2]))
-        _lib.check(
-            lib.pk_attn_varlen_bwd(
-                q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
-                ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), strides, num_seqs,
-                total, longest, q_heads, k.shape[1], head_dim, _scale(head_dim, softmax_scale), int(causal),
-                _lib.dtype_code(q.dtype), _lib.stream_handle(q.device),
-            ),
-            lib,
-        )
+        with _lib.on_device(q.device):
+            _lib.check(
+                lib.pk_attn_varlen_bwd(
+                    q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr(), do_.data_ptr(), lse.data_ptr(),
+                    ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), strides,
+                    num_seqs, total, longest, q_heads, k.shape[1], head_dim, _scale(head_dim, softmax_scale),
+                    int(causal), _lib.dtype_code(q.dtype), _lib.stream_handle(q.device),
+                ),
+                lib,
+            )
         return dq, dk, dv, None, None, None, None, None
