@@ -53,6 +53,14 @@ def _same_dtype(name: str, *tensors: Tensor | None) -> torch.dtype:
 _HALF = (torch.bfloat16, torch.float16)
 
 
+def _tracks_grad(*tensors: Tensor | None) -> bool:
+    """Whether autograd must record the call: grad mode on and some input requiring grad.
+
+    Calls that need no graph skip the autograd node (one launch, nothing saved).
+    """
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
 def _norm_dtypes(name: str, x: Tensor, weight: Tensor, bias: Tensor | None) -> tuple[torch.dtype, torch.dtype]:
     """(x dtype, weight dtype): one dtype, or a 16-bit x with fp32 weight (and bias), whose product promotes to fp32."""
     if bias is not None and bias.dtype != weight.dtype:
@@ -170,8 +178,7 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
     (the weight's). Without a gradient to track, the call is one launch with no
     autograd node and no saved statistics.
     """
-    if torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad
-                                    or (bias is not None and bias.requires_grad)):
+    if _tracks_grad(x, weight, bias):
         return _RMSNorm.apply(x, weight, bias, eps)
     return _rms_norm_fwd(x, weight, bias, eps, want_rstd=False)[0]
 
@@ -179,32 +186,38 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
 # --------------------------------------------------------------------------- add_rms_norm
 
 
+def _add_rms_norm_fwd(x: Tensor, residual: Tensor, weight: Tensor, eps: float, offset: float):
+    """One pk_add_rmsnorm_fwd launch: (y, s) as [rows, cols], the weight and rstd."""
+    device = _require_cuda(x, residual, weight)
+    dtype = _same_dtype("add_rms_norm", x, residual, weight)
+    cols = x.shape[-1]
+    if residual.shape != x.shape:
+        raise ValueError(f"popcorn_amd.add_rms_norm: residual {tuple(residual.shape)} != x {tuple(x.shape)}")
+    if weight.shape != (cols,):
+        raise ValueError(f"popcorn_amd.add_rms_norm: weight must be [{cols}]")
+    x2 = x.reshape(-1, cols).contiguous()
+    r2 = residual.reshape(-1, cols).contiguous()
+    w = weight.contiguous()
+    rows = x2.shape[0]
+    y = torch.empty_like(x2)
+    s = torch.empty_like(x2)
+    rstd = torch.empty(rows, dtype=torch.float32, device=device)
+    lib = _lib.load()
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_add_rmsnorm_fwd(
+                x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
+                float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
+            ),
+            lib,
+        )
+    return y, s, w, rstd
+
+
 class _AddRMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, residual: Tensor, weight: Tensor, eps: float, offset: float):
-        device = _require_cuda(x, residual, weight)
-        dtype = _same_dtype("add_rms_norm", x, residual, weight)
-        cols = x.shape[-1]
-        if residual.shape != x.shape:
-            raise ValueError(f"popcorn_amd.add_rms_norm: residual {tuple(residual.shape)} != x {tuple(x.shape)}")
-        if weight.shape != (cols,):
-            raise ValueError(f"popcorn_amd.add_rms_norm: weight must be [{cols}]")
-        x2 = x.reshape(-1, cols).contiguous()
-        r2 = residual.reshape(-1, cols).contiguous()
-        w = weight.contiguous()
-        rows = x2.shape[0]
-        y = torch.empty_like(x2)
-        s = torch.empty_like(x2)
-        rstd = torch.empty(rows, dtype=torch.float32, device=device)
-        lib = _lib.load()
-        with _lib.on_device(device):
-            _lib.check(
-                lib.pk_add_rmsnorm_fwd(
-                    x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
-                    float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
-                ),
-                lib,
-            )
+        y, s, w, rstd = _add_rms_norm_fwd(x, residual, weight, eps, offset)
         ctx.save_for_backward(s, w, rstd)
         ctx.offset = float(offset)
         ctx.shape = x.shape
@@ -249,30 +262,39 @@ def add_rms_norm(x: Tensor, residual: Tensor, weight: Tensor, eps: float = 1e-6,
     x, residual [..., hidden]; weight [hidden]; one dtype for all. Backward gives
     d(x) = d(residual) and dweight.
     """
-    return _AddRMSNorm.apply(x, residual, weight, eps, offset)
+    if _tracks_grad(x, residual, weight):
+        return _AddRMSNorm.apply(x, residual, weight, eps, offset)
+    y, s, _, _ = _add_rms_norm_fwd(x, residual, weight, eps, offset)
+    return y.view(x.shape), s.view(x.shape)
 
 
 # --------------------------------------------------------------------------- swiglu
 
 
+def _swiglu_fwd(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """One pk_swiglu_fwd launch: (y, a and b as the contiguous tensors it read)."""
+    device = _require_cuda(a, b)
+    dtype = _same_dtype("swiglu", a, b)
+    if a.shape != b.shape:
+        raise ValueError(f"popcorn_amd.swiglu: shapes differ {tuple(a.shape)} vs {tuple(b.shape)}")
+    a_c, b_c = a.contiguous(), b.contiguous()
+    y = torch.empty_like(a_c)
+    lib = _lib.load()
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_swiglu_fwd(
+                a_c.data_ptr(), b_c.data_ptr(), y.data_ptr(), a_c.numel(), _lib.dtype_code(dtype),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
+    return y, a_c, b_c
+
+
 class _SwiGLU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, a: Tensor, b: Tensor) -> Tensor:
-        device = _require_cuda(a, b)
-        dtype = _same_dtype("swiglu", a, b)
-        if a.shape != b.shape:
-            raise ValueError(f"popcorn_amd.swiglu: shapes differ {tuple(a.shape)} vs {tuple(b.shape)}")
-        a_c, b_c = a.contiguous(), b.contiguous()
-        y = torch.empty_like(a_c)
-        lib = _lib.load()
-        with _lib.on_device(device):
-            _lib.check(
-                lib.pk_swiglu_fwd(
-                    a_c.data_ptr(), b_c.data_ptr(), y.data_ptr(), a_c.numel(), _lib.dtype_code(dtype),
-                    _lib.stream_handle(device),
-                ),
-                lib,
-            )
+        y, a_c, b_c = _swiglu_fwd(a, b)
         ctx.save_for_backward(a_c, b_c)
         return y
 
@@ -295,7 +317,9 @@ class _SwiGLU(torch.autograd.Function):
 
 def swiglu(a: Tensor, b: Tensor) -> Tensor:
     """y = silu(a) * b elementwise (a, b of one shape and dtype); differentiable."""
-    return _SwiGLU.apply(a, b)
+    if _tracks_grad(a, b):
+        return _SwiGLU.apply(a, b)
+    return _swiglu_fwd(a, b)[0]
 
 
 # --------------------------------------------------------------------------- rotary
@@ -342,13 +366,19 @@ def _last_contiguous(t: Tensor) -> Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _rotary_fwd(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """One pk_rotary launch into a new tensor: (y, cos, sin as the contiguous tables it read)."""
+    xs = _last_contiguous(x.detach())
+    cos_c, sin_c = cos.detach().contiguous(), sin.detach().contiguous()
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _rotate(xs, cos_c, sin_c, y, interleaved, conjugate=False)
+    return y, cos_c, sin_c
+
+
 class _Rotary(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool) -> Tensor:
-        xs = _last_contiguous(x)
-        cos_c, sin_c = cos.detach().contiguous(), sin.detach().contiguous()
-        y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-        _rotate(xs, cos_c, sin_c, y, interleaved, conjugate=False)
+        y, cos_c, sin_c = _rotary_fwd(x, cos, sin, interleaved)
         ctx.save_for_backward(cos_c, sin_c)
         ctx.interleaved = interleaved
         return y
@@ -368,7 +398,9 @@ def rotary_embedding(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = Fa
     NeoX halves by default, GPT-J pairs with interleaved=True; channels past
     2*half are passed through. Returns a new tensor; cos and sin get no gradient.
     """
-    return _Rotary.apply(x, cos, sin, interleaved)
+    if _tracks_grad(x):
+        return _Rotary.apply(x, cos, sin, interleaved)
+    return _rotary_fwd(x, cos, sin, interleaved)[0]
 
 
 def rotary_embedding_(x: Tensor, cos: Tensor, sin: Tensor, interleaved: bool = False) -> Tensor:
@@ -454,7 +486,9 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
     row may differ. fp32 arithmetic, one rounding per output; one launch for q
     and k. Gradients have q/k's dtype; cos and sin get none.
     """
-    return _Rope.apply(q, k, cos, sin)
+    if _tracks_grad(q, k):
+        return _Rope.apply(q, k, cos, sin)
+    return _rope(q, k, cos, sin, transpose=False)
 
 
 def _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin):
@@ -480,32 +514,38 @@ def _dense(t: Tensor) -> Tensor:
     return c if c.data_ptr() % 16 == 0 else c.clone()
 
 
+def _qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps):
+    """One pk_qk_norm_rope_fwd launch: (yq, yk, and what the backward reads: q, k, weights, tables, rstd)."""
+    device, dtype, batch, seq, head_dim = _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin)
+    q_, k_ = _aligned_rows(q.detach()), _aligned_rows(k.detach())
+    qw, kw, cs, sn = (_dense(t) for t in (q_weight, k_weight, cos, sin))
+    out_dtype = torch.promote_types(dtype, cs.dtype)
+    yq = torch.empty(q.shape, dtype=out_dtype, device=device)
+    yk = torch.empty(k.shape, dtype=out_dtype, device=device)
+    rq = torch.empty((batch, q.shape[1], seq), dtype=torch.float32, device=device)
+    rk = torch.empty((batch, k.shape[1], seq), dtype=torch.float32, device=device)
+    lib = _lib.load()
+    st = (_lib._i64 * 12)(*(x for t in (q_, k_, yq, yk) for x in t.stride()[:3]))
+    code = _lib.dtype_code(dtype)
+    with _lib.on_device(device):
+        _lib.check(
+            lib.pk_qk_norm_rope_fwd(
+                q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
+                yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
+                head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
+                _lib.stream_handle(device),
+            ),
+            lib,
+        )
+    return yq, yk, (q_, k_, qw, kw, cs, sn, rq, rk)
+
+
 class _QkNormRope(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, q_weight, k_weight, cos, sin, eps):
-        device, dtype, batch, seq, head_dim = _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin)
-        q_, k_ = _aligned_rows(q.detach()), _aligned_rows(k.detach())
-        qw, kw, cs, sn = (_dense(t) for t in (q_weight, k_weight, cos, sin))
-        out_dtype = torch.promote_types(dtype, cs.dtype)
-        yq = torch.empty(q.shape, dtype=out_dtype, device=device)
-        yk = torch.empty(k.shape, dtype=out_dtype, device=device)
-        rq = torch.empty((batch, q.shape[1], seq), dtype=torch.float32, device=device)
-        rk = torch.empty((batch, k.shape[1], seq), dtype=torch.float32, device=device)
-        lib = _lib.load()
-        st = (_lib._i64 * 12)(*(x for t in (q_, k_, yq, yk) for x in t.stride()[:3]))
-        code = _lib.dtype_code(dtype)
-        with _lib.on_device(device):
-            _lib.check(
-                lib.pk_qk_norm_rope_fwd(
-                    q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
-                    yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
-                    head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
-                    _lib.stream_handle(device),
-                ),
-                lib,
-            )
-        ctx.save_for_backward(q_, k_, qw, kw, cs, sn, rq, rk)
-        ctx.out_dtype = out_dtype
+        yq, yk, saved = _qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps)
+        ctx.out_dtype = yq.dtype
+        ctx.save_for_backward(*saved)
         return yq, yk
 
     @staticmethod
@@ -550,7 +590,9 @@ def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, cos: 
     per output. Backward gives dq, dk and the two weight gradients in q's
     dtype; cos and sin get none.
     """
-    return _QkNormRope.apply(q, k, q_weight, k_weight, cos, sin, eps)
+    if _tracks_grad(q, k, q_weight, k_weight):
+        return _QkNormRope.apply(q, k, q_weight, k_weight, cos, sin, eps)
+    return _qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps)[:2]
 
 
 # --------------------------------------------------------------------------- attention
@@ -570,7 +612,7 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
     bf16 or fp16; head_dim 64 or 128; scale defaults to head_dim ** -0.5.
     Backward gives dq, dk, dv.
     """
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+    if _tracks_grad(q, k, v):
         return _Attention.apply(q, k, v, causal, softmax_scale)
     return _attn_fwd(q, k, v, causal, softmax_scale, want_lse=False)[0]
 
@@ -668,7 +710,7 @@ def attn_varlen(
     gives dq, dk, dv.
     """
     cu, num_seqs, longest = _cut_points(cu_seqlens, q.shape[0], q.device)
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+    if _tracks_grad(q, k, v):
         return _AttentionVarlen.apply(q, k, v, cu, num_seqs, longest, causal, softmax_scale)
     return _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=False)[0]
 
