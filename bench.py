@@ -374,7 +374,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         dw = torch.empty_like(w)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         _lib.check(lib.pk_add_rmsnorm_fwd(x.data_ptr(), res.data_ptr(), w.data_ptr(), y.data_ptr(), sm.data_ptr(),
-                                          rstd.data_ptr(), rows, cols, 1e-6, 1.0, _lib.BF16, stream()))
+                                          rstd.data_ptr(), rows, cols, 1e-6, 1.0, _lib.BF16, _lib.BF16, stream()))
         ws_bytes = lib.pk_rmsnorm_bwd_workspace(rows, cols, _lib.BF16)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
@@ -385,7 +385,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         def launch(i):
             _lib.check(lib.pk_add_rmsnorm_bwd(sm.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr(),
                                               ds.data_ptr(), dsum.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws_bytes,
-                                              rows, cols, 1.0, _lib.BF16, stream()))
+                                              rows, cols, 1.0, _lib.BF16, _lib.BF16, stream()))
 
         def cpu():
             sample = rows

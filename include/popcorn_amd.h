@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define PK_ABI_VERSION 4
+#define PK_ABI_VERSION 5
 
 /* status codes */
 #define PK_OK 0
@@ -115,23 +115,27 @@ int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, cons
  *   s = round(x + residual); r = 1/sqrt(mean(s^2) + eps);
  *   y = round(round(s*r) * round(w + offset)).
  * Writes y and s (the new residual stream); rstd (fp32 [rows]) may be NULL.
- * All tensors share `dtype`. Replaces: reference `add_rms_norm`
- * (kernels/add_rms_norm.py:8-26, `s = x + residual; rms(s, eps) * (weight + offset)`).
+ * x, residual and s have `dtype`; w and y have `w_dtype`: `dtype`, or fp32
+ * with a 16-bit `dtype` (torch's promotion: w + offset stays fp32 and the
+ * product with the rounded 16-bit row is an fp32 y). Replaces: reference
+ * `add_rms_norm` (kernels/add_rms_norm.py:8-26,
+ * `s = x + residual; rms(s, eps) * (weight + offset)`).
  */
 int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y, void* s, float* rstd,
-                       int64_t rows, int64_t cols, float eps, float offset, int dtype, void* stream);
+                       int64_t rows, int64_t cols, float eps, float offset, int dtype, int w_dtype, void* stream);
 
 /*
  * Backward of pk_add_rmsnorm_fwd. With n = s*r, u = dy*(w + offset):
  *   ds_total = r*(u - n*mean(u*n)) + ds,  dw = sum_rows dy*n,
  * where ds is the gradient reaching s through the second output (may be
- * NULL). ds_total is the gradient of both x and residual (dx). The workspace
- * is sized by pk_rmsnorm_bwd_workspace. Replaces torch autograd of the
- * reference (kernels/add_rms_norm.py:25-26).
+ * NULL). ds_total is the gradient of both x and residual (dx). s, ds and dx
+ * have `dtype`; w, dy and dw have `w_dtype` (as pk_add_rmsnorm_fwd). The
+ * workspace is sized by pk_rmsnorm_bwd_workspace. Replaces torch autograd of
+ * the reference (kernels/add_rms_norm.py:25-26).
  */
 int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const void* dy, const void* ds, void* dx,
                        void* dw, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, float offset,
-                       int dtype, void* stream);
+                       int dtype, int w_dtype, void* stream);
 
 /*
  * Rotary embedding of x [batch, seq, heads, head_dim] with tables

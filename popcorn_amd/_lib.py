@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "libpopcorn_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, BF16, F16 = 0, 1, 2
@@ -36,8 +36,8 @@ SIGNATURES = {
     "pk_rmsnorm_bwd_workspace": (_i64, [_i64, _i64, _int]),
     "pk_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _p]),
     "pk_rmsnorm_bwd_noalloc": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
-    "pk_add_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _int, _p]),
-    "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _p]),
+    "pk_add_rmsnorm_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _int, _int, _p]),
+    "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_rotary": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
     "pk_rope": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
     "pk_qk_norm_rope_fwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _int, _p]),

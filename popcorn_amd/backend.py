@@ -63,8 +63,9 @@ def rms_norm_supported(x, weight, bias, eps) -> bool:
 def add_rms_norm_supported(x, residual, weight, eps, offset) -> bool:
     return (
         _on_hip(x, residual, weight)
-        and x.dtype == residual.dtype == weight.dtype
+        and x.dtype == residual.dtype
         and x.dtype in _FLOATS
+        and (weight.dtype == x.dtype or (x.dtype in _HALF and weight.dtype == torch.float32))
         and x.shape == residual.shape
         and x.shape[-1] > 0
     )

@@ -659,19 +659,17 @@ template <typename T, typename W, int MODE> Layout layout_for(int64_t rows, int6
   return l;
 }
 
-// (x dtype, weight dtype) pairs the kernels implement: one dtype, or a 16-bit x
-// with an fp32 weight (not in the residual-add mode, whose reference adds at
-// one dtype).
-bool supported_pair(int dtype, int wdtype, int mode) {
+// (x dtype, weight dtype) pairs the kernels implement, in every mode: one
+// dtype, or a 16-bit x (with its residual and sum, in the residual-add mode)
+// with an fp32 weight.
+bool supported_pair(int dtype, int wdtype, int /*mode*/) {
   if (wdtype == dtype) return known_dtype(dtype);
-  return mode != kAdd && wdtype == PK_F32 && (dtype == PK_BF16 || dtype == PK_F16);
+  return wdtype == PK_F32 && (dtype == PK_BF16 || dtype == PK_F16);
 }
 
 template <int MODE> Layout layout_of(int64_t rows, int64_t cols, int dtype, int wdtype) {
-  if constexpr (MODE != kAdd) {
-    if (wdtype != dtype) return dtype == PK_BF16 ? layout_for<bf16, float, MODE>(rows, cols)
-                                                 : layout_for<f16, float, MODE>(rows, cols);
-  }
+  if (wdtype != dtype) return dtype == PK_BF16 ? layout_for<bf16, float, MODE>(rows, cols)
+                                               : layout_for<f16, float, MODE>(rows, cols);
   switch (dtype) {
     case PK_F32: return layout_for<float, float, MODE>(rows, cols);
     case PK_BF16: return layout_for<bf16, bf16, MODE>(rows, cols);
@@ -698,9 +696,7 @@ int64_t workspace_bytes(int64_t rows, int64_t cols, int dtype) {
 }
 
 template <int MODE> int fwd_dispatch(const FwdArgs& a, int dtype, int wdtype, const char* who) {
-  if constexpr (MODE != kAdd) {
-    if (wdtype != dtype) return dtype == PK_BF16 ? fwd<bf16, float, MODE>(a, who) : fwd<f16, float, MODE>(a, who);
-  }
+  if (wdtype != dtype) return dtype == PK_BF16 ? fwd<bf16, float, MODE>(a, who) : fwd<f16, float, MODE>(a, who);
   switch (dtype) {
     case PK_F32: return fwd<float, float, MODE>(a, who);
     case PK_BF16: return fwd<bf16, bf16, MODE>(a, who);
@@ -709,9 +705,7 @@ template <int MODE> int fwd_dispatch(const FwdArgs& a, int dtype, int wdtype, co
 }
 
 template <int MODE> int bwd_dispatch(const BwdArgs& a, int dtype, int wdtype, const char* who) {
-  if constexpr (MODE != kAdd) {
-    if (wdtype != dtype) return dtype == PK_BF16 ? bwd<bf16, float, MODE>(a, who) : bwd<f16, float, MODE>(a, who);
-  }
+  if (wdtype != dtype) return dtype == PK_BF16 ? bwd<bf16, float, MODE>(a, who) : bwd<f16, float, MODE>(a, who);
   switch (dtype) {
     case PK_F32: return bwd<float, float, MODE>(a, who);
     case PK_BF16: return bwd<bf16, bf16, MODE>(a, who);
@@ -848,24 +842,24 @@ int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, cons
 }
 
 int pk_add_rmsnorm_fwd(const void* x, const void* residual, const void* w, void* y, void* s, float* rstd,
-                       int64_t rows, int64_t cols, float eps, float offset, int dtype, void* stream) {
+                       int64_t rows, int64_t cols, float eps, float offset, int dtype, int w_dtype, void* stream) {
   using namespace pk;
   const char* who = "pk_add_rmsnorm_fwd";
-  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (int st = check_shape(who, rows, cols, dtype, w_dtype, kAdd)) return st;
   if (rows == 0) return PK_OK;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: zero-width rows");
   if (!x || !residual || !w || !y || !s) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: null pointer");
   if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_fwd: offset is not finite");
   const FwdArgs a{x, w, nullptr, residual, s, offset, y, rstd, rows, (int)cols, eps, static_cast<hipStream_t>(stream)};
-  return fwd_dispatch<kAdd>(a, dtype, dtype, who);
+  return fwd_dispatch<kAdd>(a, dtype, w_dtype, who);
 }
 
 int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const void* dy, const void* ds, void* dx,
                        void* dw, void* workspace, int64_t workspace_bytes, int64_t rows, int64_t cols, float offset,
-                       int dtype, void* stream) {
+                       int dtype, int w_dtype, void* stream) {
   using namespace pk;
   const char* who = "pk_add_rmsnorm_bwd";
-  if (int st = check_shape(who, rows, cols, dtype)) return st;
+  if (int st = check_shape(who, rows, cols, dtype, w_dtype, kAdd)) return st;
   if (cols == 0) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: zero-width rows");
   if (!s || !w || !rstd || !dy || !dx || !dw || !workspace)
     return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: null pointer");
@@ -873,8 +867,8 @@ int pk_add_rmsnorm_bwd(const void* s, const void* w, const float* rstd, const vo
   if (!isfinite(offset)) return fail(PK_ERR_INVALID, "pk_add_rmsnorm_bwd: offset is not finite");
   BwdArgs a{s, w, dy, ds, offset, rstd, dx, dw, nullptr, nullptr, nullptr, nullptr, rows, (int)cols,
             static_cast<hipStream_t>(stream)};
-  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, dtype, kAdd, a)) return st;
-  return bwd_dispatch<kAdd>(a, dtype, dtype, who);
+  if (int st = carve(who, workspace, workspace_bytes, rows, cols, dtype, w_dtype, kAdd, a)) return st;
+  return bwd_dispatch<kAdd>(a, dtype, w_dtype, who);
 }
 
 }  // extern "C"

@@ -189,7 +189,9 @@ def rms_norm(x: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float =
 def _add_rms_norm_fwd(x: Tensor, residual: Tensor, weight: Tensor, eps: float, offset: float):
     """One pk_add_rmsnorm_fwd launch: (y, s) as [rows, cols], the weight and rstd."""
     device = _require_cuda(x, residual, weight)
-    dtype = _same_dtype("add_rms_norm", x, residual, weight)
+    if residual.dtype != x.dtype:
+        raise TypeError(f"popcorn_amd.add_rms_norm: residual {residual.dtype} differs from x {x.dtype}")
+    dtype, wdtype = _norm_dtypes("add_rms_norm", x, weight, None)
     cols = x.shape[-1]
     if residual.shape != x.shape:
         raise ValueError(f"popcorn_amd.add_rms_norm: residual {tuple(residual.shape)} != x {tuple(x.shape)}")
@@ -199,7 +201,7 @@ def _add_rms_norm_fwd(x: Tensor, residual: Tensor, weight: Tensor, eps: float, o
     r2 = residual.reshape(-1, cols).contiguous()
     w = weight.contiguous()
     rows = x2.shape[0]
-    y = torch.empty_like(x2)
+    y = torch.empty((rows, cols), dtype=wdtype, device=device)
     s = torch.empty_like(x2)
     rstd = torch.empty(rows, dtype=torch.float32, device=device)
     lib = _lib.load()
@@ -207,7 +209,7 @@ def _add_rms_norm_fwd(x: Tensor, residual: Tensor, weight: Tensor, eps: float, o
         _lib.check(
             lib.pk_add_rmsnorm_fwd(
                 x2.data_ptr(), r2.data_ptr(), w.data_ptr(), y.data_ptr(), s.data_ptr(), rstd.data_ptr(), rows, cols,
-                float(eps), float(offset), _lib.dtype_code(dtype), _lib.stream_handle(device),
+                float(eps), float(offset), _lib.dtype_code(dtype), _lib.dtype_code(wdtype), _lib.stream_handle(device),
             ),
             lib,
         )
@@ -231,7 +233,7 @@ class _AddRMSNorm(torch.autograd.Function):
         if dy is None:  # only the residual stream was used downstream
             dsum = ds.reshape(rows, cols).to(s.dtype) if ds is not None else torch.zeros_like(s)
             return dsum.view(ctx.shape), dsum.view(ctx.shape), torch.zeros_like(w), None, None
-        dy2 = dy.reshape(rows, cols).to(s.dtype).contiguous()
+        dy2 = dy.reshape(rows, cols).to(w.dtype).contiguous()
         ds2 = ds.reshape(rows, cols).to(s.dtype).contiguous() if ds is not None else None
         dsum = torch.empty_like(s)
         dw = torch.empty_like(w)
@@ -247,7 +249,8 @@ class _AddRMSNorm(torch.autograd.Function):
                     lib.pk_add_rmsnorm_bwd(
                         s.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy2.data_ptr(),
                         ds2.data_ptr() if ds2 is not None else None, dsum.data_ptr(), dw.data_ptr(),
-                        workspace.data_ptr(), nbytes, rows, cols, ctx.offset, code, _lib.stream_handle(s.device),
+                        workspace.data_ptr(), nbytes, rows, cols, ctx.offset, code, _lib.dtype_code(w.dtype),
+                        _lib.stream_handle(s.device),
                     ),
                     lib,
                 )
@@ -259,8 +262,10 @@ def add_rms_norm(x: Tensor, residual: Tensor, weight: Tensor, eps: float = 1e-6,
                  offset: float = 0.0) -> tuple[Tensor, Tensor]:
     """(y, s): s = round(x + residual), y = round(round(s * rsqrt(mean(s^2) + eps)) * round(weight + offset)).
 
-    x, residual [..., hidden]; weight [hidden]; one dtype for all. Backward gives
-    d(x) = d(residual) and dweight.
+    x, residual [..., hidden]; weight [hidden]; one dtype for all, or 16-bit x and
+    residual with an fp32 weight, where y promotes to fp32 and s keeps x's dtype
+    (kernels/add_rms_norm.py:26). Backward gives d(x) = d(residual) in x's dtype
+    and dweight in the weight's.
     """
     if _tracks_grad(x, residual, weight):
         return _AddRMSNorm.apply(x, residual, weight, eps, offset)

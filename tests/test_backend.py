@@ -60,6 +60,9 @@ def test_predicates_cover_the_mixed_dtype_pairs(monkeypatch):
     assert not backend.rms_norm_supported(x, t(64, dtype=f32), t(64, dtype=bf), 1e-6)
     assert not backend.rms_norm_supported(t(4, 64, dtype=f32), t(64, dtype=bf), None, 1e-6)
     assert not backend.rms_norm_supported(x, t(64, dtype=f16), None, 1e-6)
+    assert backend.add_rms_norm_supported(x, x, t(64, dtype=f32), 1e-6, 0.0)
+    assert not backend.add_rms_norm_supported(x, t(4, 64, dtype=f32), t(64, dtype=f32), 1e-6, 0.0)
+    assert not backend.add_rms_norm_supported(t(4, 64, dtype=f32), t(4, 64, dtype=f32), t(64, dtype=bf), 1e-6, 0.0)
 
     q, k = t(2, 4, 8, 64, dtype=bf), t(2, 2, 8, 64, dtype=bf)
     for table in (bf, f16, f32):

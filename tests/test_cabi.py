@@ -84,12 +84,14 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     rot = (ctypes.c_int64 * 6)(*([128] * 6))
     rc = lib.pk_rotary(None, None, None, None, rot, 1, 4, 2, 128, 80, _lib.BF16, _lib.F32, 0, 0, None)
     assert rc == _lib.ERR_INVALID and "half" in lib.pk_last_error().decode()
-    rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, _lib.BF16, None)
+    rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, _lib.BF16, _lib.BF16, None)
     assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
-    assert lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 0, 64, 1e-6, 0.0, _lib.BF16, None) == _lib.OK
-    rc = lib.pk_add_rmsnorm_bwd(None, None, None, None, None, None, None, None, 0, 4, 64, 1.0, _lib.BF16, None)
+    assert lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 0, 64, 1e-6, 0.0, _lib.BF16, _lib.BF16,
+                                  None) == _lib.OK
+    rc = lib.pk_add_rmsnorm_bwd(None, None, None, None, None, None, None, None, 0, 4, 64, 1.0, _lib.BF16, _lib.BF16,
+                                None)
     assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
-    rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, 9, None)
+    rc = lib.pk_add_rmsnorm_fwd(None, None, None, None, None, None, 4, 64, 1e-6, 0.0, 9, 9, None)
     assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
     rs = (ctypes.c_int64 * 12)(*([64] * 12))
     rc = lib.pk_rope(None, None, None, None, None, None, rs, 2, 4, 2, 8, 63, 1, _lib.BF16, _lib.BF16, _lib.BF16, 0, None)

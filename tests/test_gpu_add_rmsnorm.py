@@ -19,12 +19,14 @@ def _device():
         pytest.skip("no HIP device")
 
 
-def _run(shape, dtype, eps, offset, seed, with_ds=True):
+def _run(shape, dtype, eps, offset, seed, with_ds=True, wdtype=None):
+    """x, residual and s in `dtype`; weight, y and y's cotangent in `wdtype` (default `dtype`)."""
+    wdtype = dtype if wdtype is None else wdtype
     cols = shape[-1]
     x = seeded(shape, seed, dtype)
     res = seeded(shape, seed + 1, dtype)
-    w = (1 + 0.1 * seeded((cols,), seed + 2, torch.float32)).to(dtype)
-    dy = seeded(shape, 1000 + seed, dtype)
+    w = (1 + 0.1 * seeded((cols,), seed + 2, torch.float32)).to(wdtype)
+    dy = seeded(shape, 1000 + seed, wdtype)
     ds = seeded(shape, 2000 + seed, dtype) if with_ds else None
 
     n64 = [t.double().numpy() for t in (x, res, w, dy)]
@@ -41,14 +43,16 @@ def _run(shape, dtype, eps, offset, seed, with_ds=True):
     outs_m, cots_m = ([ym, sm], [dy.to(DEV), ds.to(DEV)]) if with_ds else ([ym], [dy.to(DEV)])
     grads_m = torch.autograd.grad(outs_m, mine, cots_m)
 
-    assert ym.shape == x.shape and ym.dtype == dtype and sm.shape == x.shape and sm.dtype == dtype
+    assert ym.shape == x.shape and ym.dtype == yr.dtype == wdtype and sm.shape == x.shape and sm.dtype == dtype
+    assert [t.dtype for t in grads_m] == [t.dtype for t in grads_r] == [dtype, dtype, wdtype]
     # s is torch's own add at the native dtype: bit for bit
     assert torch.equal(sm.cpu(), (x + res)), "s differs from x + residual"
-    gauge_ok(ym, y64, yr, dtype, "y")
-    close_to_reference(ym, yr, "y")
+    gauge_ok(ym, y64, yr, wdtype, "y")
+    close_to_reference(ym, yr, "y", rounding=dtype)
     gauge_ok(sm, s64, sr, dtype, "s")
-    for got, truth, ref, name in zip(grads_m, (dx64, dres64, dw64), grads_r, ("dx", "dresidual", "dweight")):
-        gauge_ok(got, truth, ref, dtype, name)
+    for got, truth, ref, name, dt in zip(grads_m, (dx64, dres64, dw64), grads_r, ("dx", "dresidual", "dweight"),
+                                         (dtype, dtype, wdtype)):
+        gauge_ok(got, truth, ref, dt, name)
     assert torch.equal(grads_m[0], grads_m[1]), "x and residual must receive the same gradient"
 
 
@@ -63,6 +67,24 @@ SHAPES = [(1, 64), (4, 4096), (3, 1000), (17, 8192), (2, 3, 512), (300, 128), (1
 def test_add_rms_norm(shape, dtype):
     _run(shape, dtype, 1e-6, 0.0, 3)
     _run(shape, dtype, 1e-5, 1.0, 5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", [(1, 64), (4, 4096), (3, 1000), (17, 8192), (1, 7), (1030, 2048), (9001, 256)],
+                         ids=str)
+def test_add_rms_norm_16bit_x_fp32_weight(shape, dtype):
+    """Autocast's mix: 16-bit x and residual with an fp32 weight; y promotes to fp32, s keeps x's dtype."""
+    _run(shape, dtype, 1e-6, 0.0, 21, wdtype=torch.float32)
+    _run(shape, dtype, 1e-5, 1.0, 23, wdtype=torch.float32)
+    _run(shape, dtype, 1e-6, 1.0, 25, with_ds=False, wdtype=torch.float32)
+
+
+def test_add_rms_norm_mixed_pairs_outside_the_kernels_raise():
+    x = torch.ones(2, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(TypeError):
+        impls.add_rms_norm(x, x.float(), torch.ones(64, device=DEV))  # residual of another dtype
+    with pytest.raises(TypeError):
+        impls.add_rms_norm(x, x, torch.ones(64, dtype=torch.float16, device=DEV))  # bf16 x, fp16 weight
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)

@@ -180,6 +180,12 @@ def test_mixed_dtype_rms_norm_and_rope_are_served_by_the_backend():
     y = op(x, w)
     assert _selected(op) == NAME and y.dtype == torch.float32
     assert torch.equal(y, impls.rms_norm(x, w))
+    op = compat.KERNELS["add_rms_norm"]
+    r = _randn(64, 1024, seed=2)
+    y, s = op(x, r, w)
+    assert _selected(op) == NAME and y.dtype == torch.float32 and s.dtype == x.dtype
+    want = impls.add_rms_norm(x, r, w)
+    assert torch.equal(y, want[0]) and torch.equal(s, want[1])
     q, k = _randn(1, 4, 32, 128), _randn(1, 2, 32, 128, seed=1)
     ang = torch.randn(1, 32, 64, device=DEV)
     cos, sin = ang.cos().repeat(1, 1, 2), ang.sin().repeat(1, 1, 2)
