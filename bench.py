@@ -267,7 +267,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         _lib.check(lib.pk_qk_norm_rope_fwd(q.data_ptr(), k.data_ptr(), qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
                                            sin.data_ptr(), yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(),
                                            st12, B, HQ, HKV, S, D, 1, 1e-6, _lib.BF16, _lib.BF16, _lib.BF16,
-                                           stream()))
+                                           _lib.BF16, stream()))
         ws_bytes = lib.pk_qk_norm_rope_bwd_workspace(B, HQ, HKV, S, D, _lib.BF16)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         st18 = (_lib._i64 * 18)(*(x for t in (q, k, gq, gk, dq, dk) for x in t.stride()[:3]))
@@ -281,7 +281,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
                                                cos.data_ptr(), sin.data_ptr(), rq.data_ptr(), rk.data_ptr(),
                                                gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                                                dw.data_ptr(), ws.data_ptr(), ws_bytes, st18, B, HQ, HKV, S, D, 1,
-                                               _lib.BF16, _lib.BF16, _lib.BF16, stream()))
+                                               _lib.BF16, _lib.BF16, _lib.BF16, _lib.BF16, stream()))
 
         def cpu():
             qc = torch.randn(B, HQ, S, D).bfloat16().requires_grad_()

@@ -178,14 +178,16 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
  *   y = n*cos + rotate_half(n)*sin,
  * with w = q_weight [head_dim] for q rows and k_weight for k rows. fp32
  * arithmetic, one rounding per output, to y_dtype: x_dtype, or PK_F32 with
- * 16-bit inputs (fp32 tables promote the reference's rotation to fp32).
+ * 16-bit inputs (fp32 tables or fp32 weights promote the reference's
+ * rotation to fp32; with fp32 weights y_dtype must be PK_F32).
  * rstd_q [batch, q_heads, seq] and
  * rstd_k [batch, kv_heads, seq] (fp32) receive r for the backward.
  * strides[12] = q, k, yq, yk (batch, head, seq) strides in elements, all
  * multiples of the 16-byte pack (8 bf16/fp16, 4 fp32); the last dimension is
  * contiguous and every pointer 16-byte aligned. head_dim / 2 must be a pack
  * count times a power of two up to 64 (bf16: head_dim 16..1024). Weights have
- * x's dtype; cos/sin [cos_batch, seq, head_dim] as in pk_rope.
+ * w_dtype: x's, or PK_F32 with 16-bit inputs (autocast's fp32 parameters);
+ * cos/sin [cos_batch, seq, head_dim] as in pk_rope.
  * Replaces: the reference `qk_norm_rope` of examples/03_write_a_kernel.ipynb
  * (cell 3), `rms` (kernels/_utils.py:14-16) then `rope` (kernels/rope.py:23-36);
  * stands beside that notebook's Triton `_fwd` (cell 7).
@@ -193,7 +195,8 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
 int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
                         const void* sin, void* yq, void* yk, float* rstd_q, float* rstd_k, const int64_t* strides,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, void* stream);
+                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, int w_dtype,
+                        void* stream);
 
 /* Bytes of device workspace pk_qk_norm_rope_bwd needs for this shape (-1 if unsupported). */
 int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
@@ -203,7 +206,7 @@ int64_t pk_qk_norm_rope_bwd_workspace(int64_t batch, int64_t q_heads, int64_t kv
  * Backward of pk_qk_norm_rope_fwd from the inputs and the saved r:
  *   g = rotation^T(dy),  u = g*w,  dx = r*(u - x*r^2*<u, x>/head_dim),
  *   dw = sum over rows of g*x*r.
- * dw is [2, head_dim] in x's dtype: row 0 the q_weight gradient, row 1 the
+ * dw is [2, head_dim] in w_dtype: row 0 the q_weight gradient, row 1 the
  * k_weight gradient, summed deterministically through the workspace. The
  * cotangents dyq, dyk have dy_dtype (the forward's y_dtype); dq, dk x's.
  * strides[18] = q, k, dyq, dyk, dq, dk (batch, head, seq) strides.
@@ -214,7 +217,8 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
                         const void* sin, const float* rstd_q, const float* rstd_k, const void* dyq, const void* dyk,
                         void* dq, void* dk, void* dw, void* workspace, int64_t workspace_bytes,
                         const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
-                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, void* stream);
+                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, int w_dtype,
+                        void* stream);
 
 /*
  * Attention forward, o = softmax(q k^T * scale + M) v, grouped-query:

@@ -40,9 +40,9 @@ SIGNATURES = {
     "pk_add_rmsnorm_bwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_rotary": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
     "pk_rope": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
-    "pk_qk_norm_rope_fwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _int, _p]),
+    "pk_qk_norm_rope_fwd": (_int, [_p] * 10 + [_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _int, _int, _p]),
     "pk_qk_norm_rope_bwd_workspace": (_i64, [_i64, _i64, _i64, _i64, _i64, _int]),
-    "pk_qk_norm_rope_bwd": (_int, [_p] * 14 + [_i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _p]),
+    "pk_qk_norm_rope_bwd": (_int, [_p] * 14 + [_i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _int, _p]),
     "pk_attn_fwd": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_attn_bwd_workspace": (_i64, [_i64] * 5),
     "pk_attn_bwd": (_int, [_p] * 7 + [_i64] + [_p] * 4 + [_i64] * 5 + [_f32, _int, _int, _p]),

@@ -119,7 +119,9 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
     return (
         _on_hip(q, k, q_weight, k_weight, cos, sin)
         and q.dtype in _FLOATS
-        and q.dtype == k.dtype == q_weight.dtype == k_weight.dtype
+        and q.dtype == k.dtype
+        and q_weight.dtype == k_weight.dtype
+        and (q_weight.dtype == q.dtype or (q.dtype in _HALF and q_weight.dtype == torch.float32))
         and cos.dtype in _FLOATS
         and cos.dtype == sin.dtype
         and q.dim() == k.dim() == 4

@@ -312,8 +312,8 @@ __device__ __forceinline__ NormBlock norm_block(const NormArgs& a) {
   return nb;
 }
 
-// T: q, k and the weights; TO: the outputs (T, or fp32 beside fp32 tables)
-template <typename T, typename TO, typename C, int VEC, int U>
+// T: q and k; TO: the outputs (T, or fp32 beside fp32 tables or weights); W: the weights (T, or fp32)
+template <typename T, typename TO, typename C, typename W, int VEC, int U>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __restrict__ cosp,
                                                                     const C* __restrict__ sinp, NormArgs a) {
   const NormBlock nb = norm_block(a);
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __r
   table(cosp + trow + a.half, c2);
   table(sinp + trow, s1);
   table(sinp + trow + a.half, s2);
-  const T* wp = static_cast<const T*>(a.w[t]);
+  const W* wp = static_cast<const W*>(a.w[t]);
   table(wp + j, w1);
   table(wp + a.half + j, w2);
   const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
@@ -366,8 +366,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_fwd_kernel(const C* __r
   }
 }
 
-// T: q, k, the weights and their gradients; TG: the cotangents (the forward's output type)
-template <typename T, typename TG, typename C, int VEC, int U>
+// T: q, k and their gradients; TG: the cotangents (the forward's output type); W: the weights
+// and their gradients
+template <typename T, typename TG, typename C, typename W, int VEC, int U>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_bwd_kernel(const C* __restrict__ cosp,
                                                                     const C* __restrict__ sinp, NormArgs a) {
   extern __shared__ float red[];  // [4 waves][2 * half]
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_bwd_kernel(const C* __r
     table(cosp + trow + a.half, c2);
     table(sinp + trow, s1);
     table(sinp + trow + a.half, s2);
-    const T* wp = static_cast<const T*>(a.w[t]);
+    const W* wp = static_cast<const W*>(a.w[t]);
     table(wp + j, w1);
     table(wp + a.half + j, w2);
     const T* xb = static_cast<const T*>(a.x[t]) + nb.b * a.xs[t][0] + nb.s * a.xs[t][2] + j;
@@ -479,8 +480,8 @@ int64_t norm_workspace(const NormPlan& p, int64_t head_dim) {
   return up(p.blocks * cols * (int64_t)sizeof(float)) + up(stage_rows(p.blocks) * cols * (int64_t)sizeof(float));
 }
 
-// TY: the forward's output type, which is the backward's cotangent type
-template <typename T, typename TY, typename C>
+// TY: the forward's output type, which is the backward's cotangent type; W: the weights' type
+template <typename T, typename TY, typename C, typename W>
 int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const NormPlan& p, void* dw, void* ws,
                 hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
@@ -488,7 +489,7 @@ int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const
   const C* n = static_cast<const C*>(sn);
   if (!backward) {
     if (p.blocks > 0)
-      hipLaunchKernelGGL((qk_norm_rope_fwd_kernel<T, TY, C, VEC, 4>), dim3((unsigned)p.blocks), dim3(kThreads), 0, s,
+      hipLaunchKernelGGL((qk_norm_rope_fwd_kernel<T, TY, C, W, VEC, 4>), dim3((unsigned)p.blocks), dim3(kThreads), 0, s,
                          c, n, a);
     return launched("pk_qk_norm_rope_fwd");
   }
@@ -498,12 +499,12 @@ int norm_launch(bool backward, const void* cs, const void* sn, NormArgs a, const
   float* stage = reinterpret_cast<float*>(static_cast<char*>(ws) + up(p.blocks * cols * (int64_t)sizeof(float)));
   if (p.blocks > 0) {
     const size_t lds = 4 * (size_t)(2 * a.half) * sizeof(float);
-    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, TY, C, VEC, 2>), dim3((unsigned)p.blocks), dim3(kThreads), lds, s,
-                       c, n, a);
-    column_sums<T>(a.part, stage, static_cast<T*>(dw), p.blocks, cols, s);
+    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<T, TY, C, W, VEC, 2>), dim3((unsigned)p.blocks), dim3(kThreads), lds,
+                       s, c, n, a);
+    column_sums<W>(a.part, stage, static_cast<W*>(dw), p.blocks, cols, s);
   } else {  // nothing to sum: dw is zero
-    hipLaunchKernelGGL(column_sum_final<T>, dim3((cols + kFinalCols - 1) / kFinalCols), dim3(kColThreads), 0, s,
-                       stage, static_cast<T*>(dw), (int64_t)0, cols);
+    hipLaunchKernelGGL(column_sum_final<W>, dim3((cols + kFinalCols - 1) / kFinalCols), dim3(kColThreads), 0, s,
+                       stage, static_cast<W*>(dw), (int64_t)0, cols);
   }
   return launched("pk_qk_norm_rope_bwd");
 }
@@ -561,30 +562,39 @@ int norm_setup(const char* who, NormArgs& a, NormPlan& p, const void* q, const v
   return PK_OK;
 }
 
-template <typename T, typename TY>
+template <typename T, typename TY, typename W>
 int norm_run_cs(int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a, const NormPlan& p,
                 void* dw, void* ws, hipStream_t s) {
   switch (cs_dtype) {
-    case PK_F32: return norm_launch<T, TY, float>(backward, cs, sn, a, p, dw, ws, s);
-    case PK_BF16: return norm_launch<T, TY, bf16>(backward, cs, sn, a, p, dw, ws, s);
-    default: return norm_launch<T, TY, f16>(backward, cs, sn, a, p, dw, ws, s);
+    case PK_F32: return norm_launch<T, TY, float, W>(backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_launch<T, TY, bf16, W>(backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_launch<T, TY, f16, W>(backward, cs, sn, a, p, dw, ws, s);
   }
 }
 
-// The output (or cotangent) type is x's, or fp32 with a 16-bit x.
-bool norm_pair(int x_dtype, int y_dtype) {
-  return known_dtype(x_dtype) && (y_dtype == x_dtype || (y_dtype == PK_F32 && x_dtype != PK_F32));
+// Type codes the kernels take: the weights are x's type, or fp32 beside a
+// 16-bit x; the output (or cotangent) is x's type, or fp32 with a 16-bit x,
+// and fp32 whenever the weights are (their product with x promotes).
+bool norm_types(int x_dtype, int y_dtype, int w_dtype) {
+  if (!known_dtype(x_dtype)) return false;
+  const bool half = x_dtype != PK_F32;
+  if (w_dtype != x_dtype && !(half && w_dtype == PK_F32)) return false;
+  if (w_dtype != x_dtype) return y_dtype == PK_F32;
+  return y_dtype == x_dtype || (half && y_dtype == PK_F32);
 }
 
-int norm_run(int x_dtype, int y_dtype, int cs_dtype, bool backward, const void* cs, const void* sn, const NormArgs& a,
-             const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+int norm_run(int x_dtype, int y_dtype, int cs_dtype, int w_dtype, bool backward, const void* cs, const void* sn,
+             const NormArgs& a, const NormPlan& p, void* dw, void* ws, hipStream_t s) {
+  if (w_dtype != x_dtype)
+    return x_dtype == PK_BF16 ? norm_run_cs<bf16, float, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s)
+                              : norm_run_cs<f16, float, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
   if (y_dtype != x_dtype)
-    return x_dtype == PK_BF16 ? norm_run_cs<bf16, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s)
-                              : norm_run_cs<f16, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    return x_dtype == PK_BF16 ? norm_run_cs<bf16, float, bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s)
+                              : norm_run_cs<f16, float, f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
   switch (x_dtype) {
-    case PK_F32: return norm_run_cs<float, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
-    case PK_BF16: return norm_run_cs<bf16, bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
-    default: return norm_run_cs<f16, f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    case PK_F32: return norm_run_cs<float, float, float>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    case PK_BF16: return norm_run_cs<bf16, bf16, bf16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
+    default: return norm_run_cs<f16, f16, f16>(cs_dtype, backward, cs, sn, a, p, dw, ws, s);
   }
 }
 
@@ -645,11 +655,13 @@ int pk_rope(const void* q, const void* k, const void* cos, const void* sin, void
 int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, const void* k_weight, const void* cos,
                         const void* sin, void* yq, void* yk, float* rstd_q, float* rstd_k, const int64_t* strides,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
-                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, void* stream) {
+                        int64_t cos_batch, float eps, int x_dtype, int y_dtype, int cs_dtype, int w_dtype,
+                        void* stream) {
   using namespace pk;
-  if (!norm_pair(x_dtype, y_dtype))
-    return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_fwd: dtype codes %d -> %d (x's, or fp32 from 16 bits)", x_dtype,
-                y_dtype);
+  if (!norm_types(x_dtype, y_dtype, w_dtype))
+    return fail(PK_ERR_UNSUPPORTED,
+                "pk_qk_norm_rope_fwd: dtype codes %d -> %d with weights %d (x's; fp32 from 16 bits; fp32 weights "
+                "with 16 bits give fp32)", x_dtype, y_dtype, w_dtype);
   NormArgs a;
   NormPlan p;
   int rc = norm_setup("pk_qk_norm_rope_fwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 12, batch, q_heads,
@@ -670,7 +682,7 @@ int pk_qk_norm_rope_fwd(const void* q, const void* k, const void* q_weight, cons
     a.ys[1][i] = strides[9 + i];
   }
   a.eps = eps;
-  return norm_run(x_dtype, y_dtype, cs_dtype, false, cos, sin, a, p, nullptr, nullptr,
+  return norm_run(x_dtype, y_dtype, cs_dtype, w_dtype, false, cos, sin, a, p, nullptr, nullptr,
                   static_cast<hipStream_t>(stream));
 }
 
@@ -688,11 +700,13 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
                         const void* sin, const float* rstd_q, const float* rstd_k, const void* dyq, const void* dyk,
                         void* dq, void* dk, void* dw, void* workspace, int64_t workspace_bytes,
                         const int64_t* strides, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq,
-                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, void* stream) {
+                        int64_t head_dim, int64_t cos_batch, int x_dtype, int dy_dtype, int cs_dtype, int w_dtype,
+                        void* stream) {
   using namespace pk;
-  if (!norm_pair(x_dtype, dy_dtype))
-    return fail(PK_ERR_UNSUPPORTED, "pk_qk_norm_rope_bwd: dtype codes %d / %d (cotangents x's, or fp32 from 16 bits)",
-                x_dtype, dy_dtype);
+  if (!norm_types(x_dtype, dy_dtype, w_dtype))
+    return fail(PK_ERR_UNSUPPORTED,
+                "pk_qk_norm_rope_bwd: dtype codes %d / %d with weights %d (cotangents x's; fp32 from 16 bits; fp32 "
+                "with fp32 weights)", x_dtype, dy_dtype, w_dtype);
   NormArgs a;
   NormPlan p;
   int rc = norm_setup("pk_qk_norm_rope_bwd", a, p, q, k, q_weight, k_weight, cos, sin, strides, 18, batch, q_heads,
@@ -724,7 +738,8 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
       a.ys[1][i] = strides[15 + i];
     }
   }
-  return norm_run(x_dtype, dy_dtype, cs_dtype, true, cos, sin, a, p, dw, workspace, static_cast<hipStream_t>(stream));
+  return norm_run(x_dtype, dy_dtype, cs_dtype, w_dtype, true, cos, sin, a, p, dw, workspace,
+                  static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

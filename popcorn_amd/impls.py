@@ -498,7 +498,11 @@ def rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor
 
 def _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin):
     device = _require_cuda(q, k, q_weight, k_weight, cos, sin)
-    dtype = _same_dtype("qk_norm_rope", q, k, q_weight, k_weight)
+    dtype = _same_dtype("qk_norm_rope", q, k)
+    if q_weight.dtype != k_weight.dtype or not (
+            q_weight.dtype == dtype or (dtype in _HALF and q_weight.dtype == torch.float32)):
+        raise TypeError(f"popcorn_amd.qk_norm_rope: weights {q_weight.dtype}/{k_weight.dtype} with q/k {dtype} are not "
+                        "supported (q/k's dtype, or fp32 beside 16-bit q/k)")
     _table_dtype("qk_norm_rope", cos, sin)
     if q.dim() != 4 or k.dim() != 4 or cos.dim() != 3 or cos.shape != sin.shape:
         raise ValueError("popcorn_amd.qk_norm_rope: q [b, hq, s, d], k [b, hkv, s, d], cos, sin [cb, s, d] expected")
@@ -524,7 +528,7 @@ def _qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps):
     device, dtype, batch, seq, head_dim = _qk_norm_rope_shapes(q, k, q_weight, k_weight, cos, sin)
     q_, k_ = _aligned_rows(q.detach()), _aligned_rows(k.detach())
     qw, kw, cs, sn = (_dense(t) for t in (q_weight, k_weight, cos, sin))
-    out_dtype = torch.promote_types(dtype, cs.dtype)
+    out_dtype = torch.promote_types(torch.promote_types(dtype, qw.dtype), cs.dtype)
     yq = torch.empty(q.shape, dtype=out_dtype, device=device)
     yk = torch.empty(k.shape, dtype=out_dtype, device=device)
     rq = torch.empty((batch, q.shape[1], seq), dtype=torch.float32, device=device)
@@ -538,7 +542,7 @@ def _qk_norm_rope_fwd(q, k, q_weight, k_weight, cos, sin, eps):
                 q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
                 yq.data_ptr(), yk.data_ptr(), rq.data_ptr(), rk.data_ptr(), st, batch, q.shape[1], k.shape[1], seq,
                 head_dim, cos.shape[0], float(eps), code, _lib.dtype_code(out_dtype), _lib.dtype_code(cs.dtype),
-                _lib.stream_handle(device),
+                _lib.dtype_code(qw.dtype), _lib.stream_handle(device),
             ),
             lib,
         )
@@ -562,7 +566,7 @@ class _QkNormRope(torch.autograd.Function):
         gk = torch.zeros(k_.shape, dtype=gdt, device=k_.device) if gk is None else _aligned_rows(gk.to(gdt))
         dq, dk = torch.empty(q_.shape, dtype=q_.dtype, device=q_.device), torch.empty(k_.shape, dtype=k_.dtype,
                                                                                        device=k_.device)
-        dw = torch.empty((2, head_dim), dtype=q_.dtype, device=q_.device)
+        dw = torch.empty((2, head_dim), dtype=qw.dtype, device=q_.device)
         lib = _lib.load()
         code = _lib.dtype_code(q_.dtype)
         nbytes = lib.pk_qk_norm_rope_bwd_workspace(batch, q_.shape[1], k_.shape[1], seq, head_dim, code)
@@ -576,7 +580,8 @@ class _QkNormRope(torch.autograd.Function):
                     q_.data_ptr(), k_.data_ptr(), qw.data_ptr(), kw.data_ptr(), cs.data_ptr(), sn.data_ptr(),
                     rq.data_ptr(), rk.data_ptr(), gq.data_ptr(), gk.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                     dw.data_ptr(), ws.data_ptr(), nbytes, st, batch, q_.shape[1], k_.shape[1], seq, head_dim,
-                    cs.shape[0], code, _lib.dtype_code(gdt), _lib.dtype_code(cs.dtype), _lib.stream_handle(q_.device),
+                    cs.shape[0], code, _lib.dtype_code(gdt), _lib.dtype_code(cs.dtype), _lib.dtype_code(qw.dtype),
+                    _lib.stream_handle(q_.device),
                 ),
                 lib,
             )
@@ -588,12 +593,13 @@ def qk_norm_rope(q: Tensor, k: Tensor, q_weight: Tensor, k_weight: Tensor, cos: 
     """Per-head RMSNorm of q and k (weights over head_dim), then `rope`, fused into one pass.
 
     q [batch, q_heads, seq, head_dim], k [batch, kv_heads, seq, head_dim],
-    q_weight, k_weight [head_dim], cos, sin [cos_batch, seq, head_dim]; q, k and
-    the weights one dtype, cos and sin one dtype, the outputs their promotion
-    (16-bit q/k with fp32 tables give fp32); head_dim / 2 a 16-byte pack count
-    (of q's dtype) times a power of two up to 64. fp32 arithmetic, one rounding
-    per output. Backward gives dq, dk and the two weight gradients in q's
-    dtype; cos and sin get none.
+    q_weight, k_weight [head_dim], cos, sin [cos_batch, seq, head_dim]; q and k
+    one dtype, the weights q/k's dtype or fp32 beside 16-bit q/k, cos and sin one
+    dtype, the outputs the promotion of all three (16-bit q/k with fp32 tables
+    or fp32 weights give fp32); head_dim / 2 a 16-byte pack count (of q's dtype)
+    times a power of two up to 64. fp32 arithmetic, one rounding per output.
+    Backward gives dq, dk in q's dtype and the two weight gradients in the
+    weights'; cos and sin get none.
     """
     if _tracks_grad(q, k, q_weight, k_weight):
         return _QkNormRope.apply(q, k, q_weight, k_weight, cos, sin, eps)

@@ -72,5 +72,8 @@ def test_predicates_cover_the_mixed_dtype_pairs(monkeypatch):
         assert backend.qk_norm_rope_supported(q, k, w, w, cs, cs, 1e-6)
     assert not backend.rope_supported(q, t(2, 2, 8, 64, dtype=f16), t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=f32))
     assert not backend.rope_supported(q, k, t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=bf))
-    w32 = t(64, dtype=f32)
-    assert not backend.qk_norm_rope_supported(q, k, w32, w32, t(1, 8, 64, dtype=f32), t(1, 8, 64, dtype=f32), 1e-6)
+    w32, c32 = t(64, dtype=f32), t(1, 8, 64, dtype=f32)
+    assert backend.qk_norm_rope_supported(q, k, w32, w32, c32, c32, 1e-6)  # autocast's fp32 norm weights
+    assert not backend.qk_norm_rope_supported(q, k, w32, t(64, dtype=bf), c32, c32, 1e-6)
+    q32, k32 = t(2, 4, 8, 64, dtype=f32), t(2, 2, 8, 64, dtype=f32)
+    assert not backend.qk_norm_rope_supported(q32, k32, t(64, dtype=bf), t(64, dtype=bf), c32, c32, 1e-6)

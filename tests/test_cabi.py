@@ -106,7 +106,11 @@ def test_invalid_arguments_are_rejected_before_any_launch(lib):
     rc = lib.pk_rope(fake, fake, fake, fake, fake, fake, rs, 2, 4, 2, 8, 64, 1, _lib.BF16, _lib.F16, _lib.F32, 0, None)
     assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
     rc = lib.pk_qk_norm_rope_fwd(None, None, None, None, None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 1,
-                                 1e-6, _lib.F32, _lib.BF16, _lib.F32, None)
+                                 1e-6, _lib.F32, _lib.BF16, _lib.F32, _lib.F32, None)
+    assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
+    # fp32 weights beside 16-bit q/k need fp32 outputs
+    rc = lib.pk_qk_norm_rope_fwd(None, None, None, None, None, None, None, None, None, None, rs, 2, 4, 2, 8, 64, 1,
+                                 1e-6, _lib.BF16, _lib.BF16, _lib.BF16, _lib.F32, None)
     assert rc == _lib.ERR_UNSUPPORTED and "dtype" in lib.pk_last_error().decode()
     rc = lib.pk_rmsnorm_fwd(fake, fake, None, fake, None, 4, 64, 1e-6, _lib.F32, _lib.BF16, None)
     assert rc == _lib.ERR_UNSUPPORTED and "weight dtype" in lib.pk_last_error().decode()

@@ -172,7 +172,7 @@ def test_mixed_dtype_rotary_is_served_in_registration_order():
     assert torch.equal(y, impls.rotary_embedding(x, cos, sin))
 
 
-def test_mixed_dtype_rms_norm_and_rope_are_served_by_the_backend():
+def test_mixed_dtype_norms_and_rope_are_served_by_the_backend():
     """16-bit activations with fp32 weights or tables (the autocast model's calls) reach the kernels."""
     x = _randn(64, 1024)
     w = 1 + 0.1 * torch.randn(1024, device=DEV)
@@ -193,6 +193,12 @@ def test_mixed_dtype_rms_norm_and_rope_are_served_by_the_backend():
     yq, yk = op(q, k, cos, sin)
     assert _selected(op) == NAME and yq.dtype == yk.dtype == torch.float32
     want = impls.rope(q, k, cos, sin)
+    assert torch.equal(yq, want[0]) and torch.equal(yk, want[1])
+    qw, kw = 1 + 0.1 * torch.randn(128, device=DEV), 1 + 0.1 * torch.randn(128, device=DEV)
+    op = compat.KERNELS["qk_norm_rope"]
+    yq, yk = op(q, k, qw, kw, cos.bfloat16(), sin.bfloat16())
+    assert _selected(op) == NAME and yq.dtype == yk.dtype == torch.float32
+    want = impls.qk_norm_rope(q, k, qw, kw, cos.bfloat16(), sin.bfloat16())
     assert torch.equal(yq, want[0]) and torch.equal(yk, want[1])
 
 

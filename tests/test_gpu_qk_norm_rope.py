@@ -25,14 +25,17 @@ def tables(cos_batch, seq, head_dim, seed, duplicated=True):
     return draw.cos(), seeded((cos_batch, seq, head_dim), seed + 1, torch.float32).sin()
 
 
-def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicated=True, table_dtype=None):
-    """q, k, weights in `dtype`, tables in `table_dtype` (default `dtype`); outputs and cotangents in their promotion."""
+def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicated=True, table_dtype=None,
+           weight_dtype=None):
+    """q, k in `dtype`, weights in `weight_dtype` and tables in `table_dtype` (both default `dtype`); outputs and
+    cotangents in the promotion of all three, weight gradients in the weights' dtype."""
     table_dtype = dtype if table_dtype is None else table_dtype
-    out_dtype = torch.promote_types(dtype, table_dtype)
+    weight_dtype = dtype if weight_dtype is None else weight_dtype
+    out_dtype = torch.promote_types(torch.promote_types(dtype, weight_dtype), table_dtype)
     q = seeded((batch, hq, seq, d), seed, dtype)
     k = seeded((batch, hkv, seq, d), seed + 1, dtype)
-    qw = seeded((d,), seed + 6, dtype)
-    kw = seeded((d,), seed + 7, dtype)
+    qw = seeded((d,), seed + 6, weight_dtype)
+    kw = seeded((d,), seed + 7, weight_dtype)
     cos, sin = (t.to(table_dtype) for t in tables(cos_batch, seq, d, seed + 2, duplicated))
     gq, gk = seeded(tuple(q.shape), seed + 4, out_dtype), seeded(tuple(k.shape), seed + 5, out_dtype)
     n64 = lambda t: t.double().numpy()  # noqa: E731
@@ -47,7 +50,7 @@ def _check(batch, hq, hkv, seq, d, cos_batch, dtype, eps=1e-6, seed=0, duplicate
     what = f"(b {batch}, hq {hq}, hkv {hkv}, s {seq}, d {d}, cos_batch {cos_batch}, eps {eps})"
     names = ("yq", "yk", "dq", "dk", "dq_weight", "dk_weight")
     for name, got, truth, ref in zip(names, (*ym, *dm), (*y64, *d64), (*yr, *dr)):
-        want = out_dtype if name.startswith("y") else dtype
+        want = out_dtype if name.startswith("y") else weight_dtype if name.endswith("weight") else dtype
         assert got.shape == ref.shape and got.dtype == ref.dtype == want, name
         gauge_ok(got, truth, ref, want, f"{name} {what}")
     for name, got, ref in zip(("yq", "yk"), ym, yr):
@@ -76,6 +79,14 @@ def test_qk_norm_rope(case, dtype):
 def test_qk_norm_rope_fp32_tables(case, dtype):
     """16-bit q/k and weights with fp32 tables: fp32 outputs (and cotangents), 16-bit gradients."""
     _check(*case, dtype, table_dtype=torch.float32)
+
+
+@pytest.mark.parametrize("table_dtype", [None, torch.float32], ids=str)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", CASES, ids=str)
+def test_qk_norm_rope_fp32_weights(case, dtype, table_dtype):
+    """16-bit q/k with fp32 weights (autocast's norm parameters): fp32 outputs, fp32 weight gradients."""
+    _check(*case, dtype, table_dtype=table_dtype, weight_dtype=torch.float32)
 
 
 @pytest.mark.parametrize("case", [(2, 4, 2, 16, 128, 1), (1, 3, 1, 9, 8, 1), (2, 2, 1, 40, 64, 2)], ids=str)
