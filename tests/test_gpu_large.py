@@ -91,3 +91,63 @@ def test_attn_forward_past_2_31_elements_of_q():
         ref = R.attn(q[bi:bi + 1].cpu(), k[bi:bi + 1].cpu(), v[bi:bi + 1].cpu(), True)
         close_to_reference(o[bi:bi + 1], ref, f"attn batch row {bi}")
     del q, k, v, o
+
+
+def test_add_rms_norm_past_2_31_elements():
+    cols = 8192
+    rows = TWO31 // cols + 3
+    x = _randn(rows * cols, torch.bfloat16, 14).view(rows, cols).requires_grad_()
+    r = _randn(rows * cols, torch.bfloat16, 15).view(rows, cols).requires_grad_()
+    w = (1 + 0.1 * _randn(cols, torch.float32, 16)).bfloat16()
+    y, s = impls.add_rms_norm(x, r, w, 1e-6, 0.0)
+    gy = _randn(rows * cols, torch.bfloat16, 17).view(rows, cols)
+    (dx,) = torch.autograd.grad(y, (x,), gy)
+    edge = TWO31 // cols
+    for r0, r1 in ((0, 2), (edge - 2, edge + 2), (rows - 2, rows)):
+        xs, rs = (t[r0:r1].detach().cpu().requires_grad_() for t in (x, r))
+        ys, ss = R.add_rms_norm(xs, rs, w.cpu(), 1e-6, 0.0)
+        close_to_reference(s[r0:r1], ss, f"add_rms_norm s rows [{r0}, {r1})")
+        close_to_reference(y[r0:r1], ys, f"add_rms_norm y rows [{r0}, {r1})")
+        (dxs,) = torch.autograd.grad(ys, (xs,), gy[r0:r1].cpu())
+        close_to_reference(dx[r0:r1], dxs, f"add_rms_norm dx rows [{r0}, {r1})")
+    del x, r, y, s, gy, dx
+
+
+def _head_rows_across_the_boundary(heads, seq, d):
+    """(batch, head, first position) of a 10-row window of q [b, heads, seq, d] around element 2^31."""
+    row = TWO31 // d
+    bh, pos = divmod(row, seq)
+    return bh // heads, bh % heads, pos - 5
+
+
+@pytest.mark.parametrize("fused_norm", [False, True], ids=["rope", "qk_norm_rope"])
+def test_rope_and_qk_norm_rope_past_2_31_elements(fused_norm):
+    b, hq, hkv, s, d = 4, 64, 8, 65536 + 8, 128  # q holds 4 * 64 * 65544 * 128 > 2^31 elements
+    q = _randn(b * hq * s * d, torch.bfloat16, 18).view(b, hq, s, d).requires_grad_()
+    k = _randn(b * hkv * s * d, torch.bfloat16, 19).view(b, hkv, s, d).requires_grad_()
+    ang = _randn(s * d // 2, torch.float32, 20).view(1, s, d // 2).repeat(1, 1, 2)
+    cos, sin = ang.cos().bfloat16(), ang.sin().bfloat16()
+    qw = (1 + 0.1 * _randn(d, torch.float32, 21)).bfloat16()
+    kw = (1 + 0.1 * _randn(d, torch.float32, 22)).bfloat16()
+    if fused_norm:
+        yq, yk = impls.qk_norm_rope(q, k, qw, kw, cos, sin, 1e-6)
+    else:
+        yq, yk = impls.rope(q, k, cos, sin)
+    gq = _randn(b * hq * s * d, torch.bfloat16, 23).view(b, hq, s, d)
+    gk = _randn(b * hkv * s * d, torch.bfloat16, 24).view(b, hkv, s, d)
+    dq, dk = torch.autograd.grad((yq, yk), (q, k), (gq, gk))
+    eb, eh, p0 = _head_rows_across_the_boundary(hq, s, d)
+    for bi, hi, s0 in ((0, 0, 0), (eb, eh, p0), (b - 1, hq - 1, s - 10)):
+        qs = q[bi:bi + 1, hi:hi + 1, s0:s0 + 10].detach().cpu().requires_grad_()
+        ks = k[bi:bi + 1, hi % hkv:hi % hkv + 1, s0:s0 + 10].detach().cpu().requires_grad_()
+        cs, sn = cos[:, s0:s0 + 10].cpu(), sin[:, s0:s0 + 10].cpu()
+        if fused_norm:
+            rq, rk = R.qk_norm_rope(qs, ks, qw.cpu(), kw.cpu(), cs, sn, 1e-6)
+        else:
+            rq, rk = R.rope(qs, ks, cs, sn)
+        what = f"{'qk_norm_rope' if fused_norm else 'rope'} q[{bi}, {hi}, {s0}:{s0 + 10}]"
+        close_to_reference(yq[bi:bi + 1, hi:hi + 1, s0:s0 + 10], rq, what)
+        dqs, _ = torch.autograd.grad((rq, rk), (qs, ks), (gq[bi:bi + 1, hi:hi + 1, s0:s0 + 10].cpu(),
+                                                          gk[bi:bi + 1, hi % hkv:hi % hkv + 1, s0:s0 + 10].cpu()))
+        close_to_reference(dq[bi:bi + 1, hi:hi + 1, s0:s0 + 10], dqs, "d" + what)
+    del q, k, yq, yk, gq, gk, dq, dk
