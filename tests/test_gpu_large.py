@@ -77,19 +77,45 @@ def test_rotary_past_2_31_elements():
     del x, y
 
 
-def test_attn_forward_past_2_31_elements_of_q():
+def test_attn_forward_and_backward_past_2_31_elements_of_q():
     """q [4097, 32, 128, 128] holds more than 2^31 elements (short sequences, many batch rows, 16 kv
-    heads): batch rows 0 and 4096, whose first element is element 2^31, against the reference."""
+    heads): batch rows 0 and 4096, whose first element is element 2^31, against the reference,
+    forward and gradients."""
     b, s, hq, hkv, d = 4097, 32, 128, 16, 128
-    q = _randn(b * s * hq * d, torch.bfloat16, 11).view(b, s, hq, d)
-    k = _randn(b * s * hkv * d, torch.bfloat16, 12).view(b, s, hkv, d)
-    v = _randn(b * s * hkv * d, torch.bfloat16, 13).view(b, s, hkv, d)
-    with torch.no_grad():
-        o = impls.attn(q, k, v, True)
+    q = _randn(b * s * hq * d, torch.bfloat16, 11).view(b, s, hq, d).requires_grad_()
+    k = _randn(b * s * hkv * d, torch.bfloat16, 12).view(b, s, hkv, d).requires_grad_()
+    v = _randn(b * s * hkv * d, torch.bfloat16, 13).view(b, s, hkv, d).requires_grad_()
+    o = impls.attn(q, k, v, True)
+    go = _randn(b * s * hq * d, torch.bfloat16, 25).view(b, s, hq, d)
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), go)
     assert (TWO31 // (s * hq * d)) * s * hq * d == TWO31
     for bi in (0, TWO31 // (s * hq * d)):
-        ref = R.attn(q[bi:bi + 1].cpu(), k[bi:bi + 1].cpu(), v[bi:bi + 1].cpu(), True)
-        close_to_reference(o[bi:bi + 1], ref, f"attn batch row {bi}")
+        leaves = [t[bi:bi + 1].detach().cpu().float().requires_grad_() for t in (q, k, v)]
+        ref = R.attn(*leaves, True)  # fp32 on the CPU: the reference's gradients without bf16 products
+        close_to_reference(o[bi:bi + 1], ref.bfloat16(), f"attn o, batch row {bi}")
+        grads = torch.autograd.grad(ref, leaves, go[bi:bi + 1].cpu().float())
+        for name, mine, want in zip(("dq", "dk", "dv"), (dq, dk, dv), grads):
+            close_to_reference(mine[bi:bi + 1], want.bfloat16(), f"attn {name}, batch row {bi}")
+    del q, k, v, o, go, dq, dk, dv
+
+
+def test_attn_varlen_past_2_31_elements_of_q():
+    """Packed q [257 * 512 tokens, 128 heads, 128] (more than 2^31 elements) in sequences of 512:
+    the sequence holding element 2^31 and the last one against the reference."""
+    seq, n = 512, 257
+    total = seq * n
+    hq, hkv, d = 128, 8, 128
+    assert total * hq * d > TWO31
+    q = _randn(total * hq * d, torch.bfloat16, 26).view(total, hq, d)
+    k = _randn(total * hkv * d, torch.bfloat16, 27).view(total, hkv, d)
+    v = _randn(total * hkv * d, torch.bfloat16, 28).view(total, hkv, d)
+    cu = torch.arange(0, total + 1, seq, dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        o = impls.attn_varlen(q, k, v, cu, True)
+    for i in (TWO31 // (hq * d) // seq, n - 1):
+        lo, hi = i * seq, (i + 1) * seq
+        ref = R.attn(q[None, lo:hi].cpu(), k[None, lo:hi].cpu(), v[None, lo:hi].cpu(), True)[0]
+        close_to_reference(o[lo:hi], ref, f"attn_varlen sequence {i}")
     del q, k, v, o
 
 
