@@ -55,6 +55,8 @@
 // 16-lane groups) land on 64 distinct banks.
 #include <math.h>
 
+#include <type_traits>
+
 #include "api.h"
 #include "attn_common.h"
 
@@ -294,33 +296,72 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     }
   };
   const int lim = CAUSAL ? min(q_row, S - 1) : S - 1;
-  for (int t = 0; t <= n_tiles; ++t) {
-    issue(min(t + NSQ - 2, n_tiles - 1), (t + NSQ - 2) % NSQ);
-    const int u = t - 1;
-    Frag dsf[2];
-    if (u >= 0) {
-      // dS = P (dP - D), P = exp2(s c - lse2); keys a row must not see get 0
-      const int kv0 = u * BN;
-      const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > S;
+  // Tile j sits in stage j % NSQ, so step t >= 1 reads stages (t - 1) % NSQ
+  // and t % NSQ and issues into (t + 2) % NSQ. The steps are unrolled over the
+  // four stage phases: every LDS fragment address is then a lane register
+  // plus an immediate, with no per-step address arithmetic. The last step
+  // (t = n_tiles) computes S and dP of stage n_tiles % NSQ, which holds a copy
+  // of the last tile (clamped issue), and discards them.
+  auto dscores = [&](int u, Frag (&dsf)[2]) {
+    // dS = P (dP - D), P = exp2(s c - lse2); keys a row must not see get 0.
+    // The test for a mask is wave-uniform, so unmasked tiles branch past it.
+    const int kv0 = u * BN;
+    const bool need_mask = (CAUSAL && kv0 + BN - 1 > wave_first) || kv0 + BN > S;
+    if (need_mask) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int r = 8 * c + j;
-          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.c, -lse2));
-          if (need_mask) p = kv0 + 8 * (r >> 2) + 4 * g + (r & 3) <= lim ? p : 0.f;
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.c, -lse2));
+          const float p = kv0 + 8 * (r >> 2) + 4 * g + (r & 3) <= lim ? e : 0.f;
           dsf[c][j] = (T)(p * (dp[r] - dsum));
         }
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dsf[c][j] = (T)0.f;
+        for (int j = 0; j < 8; ++j) {
+          const int r = 8 * c + j;
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.c, -lse2));
+          dsf[c][j] = (T)(p * (dp[r] - dsum));
+        }
     }
-    const int sa = max(u, 0) % NSQ, sn = min(u + 1, n_tiles - 1) % NSQ;
-    run(Ks[sa], dsf, Ks[sn], Vs[sn]);  // dQ^T += K^T dS^T; S^T, dP^T of the next tile
+  };
+  auto finish = [&]() {
     loads_landed_but<(NSQ - 3) * 2 * TI>();
     __syncthreads();
+  };
+  {
+    // step 0: no dS yet (zero factors against the loaded stage 0); S^T, dP^T of tile 0
+    issue(min(NSQ - 2, n_tiles - 1), NSQ - 2);
+    Frag dsf[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dsf[c][j] = (T)0.f;
+    run(Ks[0], dsf, Ks[0], Vs[0]);
+    finish();
+  }
+  auto step = [&](int t, auto phase) {
+    constexpr int P = decltype(phase)::value;
+    constexpr int PA = (P + NSQ - 1) % NSQ;
+    issue(min(t + NSQ - 2, n_tiles - 1), (P + NSQ - 2) % NSQ);
+    Frag dsf[2];
+    dscores(t - 1, dsf);
+    run(Ks[PA], dsf, Ks[P], Vs[P]);  // dQ^T += K^T dS^T; S^T, dP^T of the next tile
+    finish();
+  };
+  static_assert(NSQ == 4, "the step loop is unrolled over four stage phases");
+  for (int t = 1;;) {
+    step(t, std::integral_constant<int, 1>{});
+    if (++t > n_tiles) break;
+    step(t, std::integral_constant<int, 2>{});
+    if (++t > n_tiles) break;
+    step(t, std::integral_constant<int, 3>{});
+    if (++t > n_tiles) break;
+    step(t, std::integral_constant<int, 0>{});
+    if (++t > n_tiles) break;
   }
   lds_loads_landed();  // tiles issued past the end, before the block's LDS is released
 
