@@ -285,13 +285,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   float l_i;  // this lane's half of the denominator
   // P = exp2(s * c - m) as the B fragments of the two 16-key steps; l += row sum
   auto softmax = [&](const f32x16& s, float m_use, Frag (&pf)[2]) {
-    float rs = 0.f;
+    float rs;  // starts at the first p, not at 0 (0 + p is an instruction)
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[8 * c + j], a.c, -m_use));
-        rs += p;
+        rs = c == 0 && j == 0 ? p : rs + p;
         pf[c][j] = (T)p;
       }
     l_i += rs;
@@ -328,14 +328,17 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // i / DT, head dims 32 * (i % DT) ..); product KK + kk is S^T step kk.
   // Fragment i + kRing is read as product i issues, and sched_barrier keeps
   // that order (the compiler would otherwise bunch the reads).
-  auto step = [&](int t) {
-    dma_k(min(t + 2, n_tiles), t & 1);
-    dma_v(min(t + 1, n_tiles - 1), (t + 1) & 1);
+  // The step is unrolled over the two buffer parities (P = t & 1), so every
+  // LDS fragment address is a lane register plus an immediate.
+  auto step = [&](int t, auto parity) {
+    constexpr int P = decltype(parity)::value;
+    dma_k(min(t + 2, n_tiles), P);
+    dma_v(min(t + 1, n_tiles - 1), P ^ 1);
     if (need_mask(t)) apply_mask(t, sc);
     softmax(sc, m_i, pf);
-    const T* ks = Ks[(t + 1) & 1] + k_lane;
+    const T* ks = Ks[P ^ 1] + k_lane;
     auto fetch = [&](int i) -> Frag {
-      if (i < KK) return vfrag(Vs[t & 1], i / DT, i % DT);
+      if (i < KK) return vfrag(Vs[P], i / DT, i % DT);
       return *reinterpret_cast<const Frag*>(ks + 16 * (i - KK));
     };
     constexpr int N = 2 * KK;  // 2 * DT == KK products of each kind
@@ -360,7 +363,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     landed();
     __syncthreads();
   };
-  for (int t = 0; t < n_tiles; ++t) step(t);
+  for (int t = 0;;) {
+    step(t, std::integral_constant<int, 0>{});
+    if (++t >= n_tiles) break;
+    step(t, std::integral_constant<int, 1>{});
+    if (++t >= n_tiles) break;
+  }
 
   {
     const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
