@@ -508,14 +508,19 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
     }
   };
 
+  // Lane offsets of the fragment reads within a stage, with the wave's half of
+  // the stage folded in: role 0 accumulates from dO (second half) and scores
+  // against Q (first half), role 1 the other way round.
+  const int a_half = role == 0 ? 0 : TILE, t_half = role == 0 ? TILE : 0;
   int a_lane[KK], t_lane[2][DT];
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) a_lane[kk] = L::at(r32, 16 * kk + 8 * g);
+  for (int kk = 0; kk < KK; ++kk) a_lane[kk] = a_half + L::at(r32, 16 * kk + 8 * g);
 #pragma unroll
   for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      t_lane[hi][dt] = L::at(8 * hi + 4 * g + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+      t_lane[hi][dt] =
+          t_half + L::at(8 * hi + 4 * g + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
 
   f32x16 acc[DT];  // dV (role 0) or dK (role 1)
 #pragma unroll
@@ -590,13 +595,21 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  for (int t = 0; t <= n_it + 1; ++t) {
+  // Step t of a wave is its local step tau = t - role (role 1 trails by one
+  // tile), working on tile u = tau - 1. For tau >= 1 it reads stages
+  // (tau - 1) % NS and tau % NS, so the steps are unrolled over the NS stage
+  // phases of tau and every fragment address is a lane register plus an
+  // immediate. Past the last tile those stages hold landed copies of it (the
+  // cursor issues the last tile again), the same data the clamped indices
+  // name. The first steps (tau <= 0, before tile 0 is scored) read stage 0.
+  auto body = [&](int t, auto a_stage, auto s_stage) {
+    constexpr int SA = decltype(a_stage)::value, SS = decltype(s_stage)::value;
     issue((t + NS - 3) % NS);
     const int u = t - 1 - role;
     const bool live = u >= 0 && u < n_it;
     Frag mf[2];
     if (live) {
-      const int st = u % NS;
+      const int st = SA;  // u % NS
       float rv[16];  // the tile rows' lse2 (role 0) or D (role 1)
       rows16(RV[st][role], rv);
       if (role == 0) {
@@ -618,7 +631,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 #pragma unroll
           for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sres[r], cs, -rv[r]));
         }
-        _Float16* pw = Pb[u & 1][slice];
+        _Float16* pw = Pb[SA & 1][slice];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           h8 hv;
@@ -632,7 +645,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
           for (int j = 0; j < 8; ++j) mf[c][j] = (T)p[8 * c + j];
       } else {
         // dS = P (dP - D), with the P role 0 left for this tile one step ago
-        const _Float16* pr = Pb[u & 1][slice];
+        const _Float16* pr = Pb[SA & 1][slice];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const h8 x = *reinterpret_cast<const h8*>(pr + 512 * j + 8 * lane);
@@ -651,11 +664,27 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
     }
     // role 0: dV^T += dO^T P and S = Q K^T of the next tile;
     // role 1: dK^T += Q^T dS and dP = dO V^T of the next tile
-    const T* ta = QG[min(max(u, 0), n_it - 1) % NS];
-    const T* ts = QG[min(max(u + 1, 0), n_it - 1) % NS];
-    run(role == 0 ? ta + TILE : ta, mf, role == 0 ? ts : ts + TILE);
+    run(QG[SA], mf, QG[SS]);
     loads_landed_but<(NS - 4) * PER_ISSUE>();
     __syncthreads();
+  };
+  using std::integral_constant;
+  int t = 0;
+  for (; t <= role; ++t) body(t, integral_constant<int, 0>{}, integral_constant<int, 0>{});  // tau <= 0
+  static_assert(NS == 6, "the step loop is unrolled over six stage phases");
+  for (;;) {  // tau = t - role >= 1, phase tau % NS = 1, 2, ..., 5, 0
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 0>{}, integral_constant<int, 1>{});
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 1>{}, integral_constant<int, 2>{});
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 2>{}, integral_constant<int, 3>{});
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 3>{}, integral_constant<int, 4>{});
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 4>{}, integral_constant<int, 5>{});
+    if (t > n_it + 1) break;
+    body(t++, integral_constant<int, 5>{}, integral_constant<int, 0>{});
   }
   loads_landed_but<0>();  // tiles issued past the end, before the block's LDS is released
 
