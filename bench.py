@@ -39,7 +39,9 @@ import torch
 HBM_PEAK_TBS = 8.0  # MI355X HBM3E, TB/s
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "achieved HBM TB/s (norm/rope/swiglu) + attn-fwd bf16 TFLOP/s, % of peak"
-FLUSH_BYTES = 512 << 20  # inputs of a workload are rotated until they exceed the 256 MB MALL twice over
+# A workload small enough to sit in the 256 MiB MALL (Infinity Cache) rotates through copies of its
+# inputs until the inputs alone span this many bytes, twice the MALL, so each launch reads from HBM.
+FLUSH_BYTES = 512 << 20
 
 # HBM bytes per launch of each workload's dominant kernel, from rocprofv3
 # FETCH_SIZE / WRITE_SIZE runs scaled by the same counters' reading for a plain
@@ -81,7 +83,7 @@ class Workload:
 
 
 def _copies(nbytes: int) -> int:
-    """Input copies to rotate so one sweep over them does not fit in the MALL."""
+    """Copies to rotate of inputs of `nbytes` per launch so that one sweep over them spans FLUSH_BYTES."""
     return max(1, math.ceil(FLUSH_BYTES / max(nbytes, 1)))
 
 
@@ -100,17 +102,21 @@ def make_workload(name: str, dev: torch.device) -> Workload:
     if name == "c1":
         rows, cols = 4096, 4096
         nbytes = rows * cols * 4 * 2 + cols * 4
-        n = _copies(nbytes)
+        # 8 copies of x (512 MiB of x alone, twice the MALL) and of y, so every launch reads its x
+        # from HBM and writes a y no recent launch wrote
+        n = _copies(rows * cols * 4)
         xs = [_randn((rows, cols), torch.float32, gen, dev) for _ in range(n)]
         w = 1 + 0.1 * _randn((cols,), torch.float32, gen, dev)
-        y = torch.empty_like(xs[0])
+        ys = [torch.empty_like(xs[0]) for _ in range(n)]
+        held = [None] * n  # the drop-in call's outputs, held so that they rotate like ys
 
         def step(i):
-            impls.rms_norm(xs[i % n], w, None, 1e-6)
+            held[i % n] = None
+            held[i % n] = impls.rms_norm(xs[i % n], w, None, 1e-6)
 
         def launch(i):
-            _lib.check(lib.pk_rmsnorm_fwd(xs[i % n].data_ptr(), w.data_ptr(), None, y.data_ptr(), None, rows, cols,
-                                          1e-6, _lib.F32, _lib.F32, stream()))
+            _lib.check(lib.pk_rmsnorm_fwd(xs[i % n].data_ptr(), w.data_ptr(), None, ys[i % n].data_ptr(), None, rows,
+                                          cols, 1e-6, _lib.F32, _lib.F32, stream()))
 
         def cpu():
             xc = torch.randn(rows, cols)
@@ -663,7 +669,7 @@ def main(argv=None) -> int:
     others = {}
     if not args.no_others and wl.name != "copy":
         del wl
-        for name in ("c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope"):
+        for name in ("c1", "c2", "c3", "c4", "c5", "attn_bwd", "add_rmsnorm", "rope", "qk_norm_rope"):
             if name == args.workload:
                 continue
             torch.cuda.empty_cache()

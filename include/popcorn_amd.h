@@ -100,7 +100,8 @@ int pk_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* 
  * summation order are pk_rmsnorm_bwd's, so the results are identical bit for
  * bit. A shape whose partial rows and stage do not fit the array (their size
  * is at most pk_rmsnorm_bwd_workspace) is refused with PK_ERR_UNSUPPORTED
- * before any launch: measured on MI355X, 65,536 rows of 8192 columns fit
+ * before any launch, and before the pointers are checked, so the limit can be
+ * probed with null pointers: measured on MI355X, 65,536 rows of 8192 columns fit
  * (69 MB), and with dbias rows of 4096 columns. Calls that overlap on one GPU
  * (other streams or threads) share the array and race; serialise them.
  * No counterpart in the reference: it is for callers that cannot allocate

@@ -13,8 +13,8 @@ Popcorn calls them directly (core/dispatcher.py:184-201).
 
 The backend's distribution is `popcorn-amd` at `popcorn_amd.__version__`
 (setup.py), pinned as both bounds of the version gate; the gate resolves for
-an installed copy, and in a source tree once `popcorn_amd.build.build()` has
-written the metadata beside the package.
+an installed copy, and in a source tree once `python -m popcorn_amd.build` (or
+`__graft_entry__.build()`) has written the metadata beside the package.
 
 The predicates only describe what the kernels cover -- tensors on a HIP
 device, one floating dtype per call, the shapes the kernels implement.

@@ -2,10 +2,12 @@
 
 `python -m popcorn_amd.build` compiles every `csrc/*.hip` to an object in
 `popcorn_amd/_build/` (in parallel) and links `popcorn_amd/libpopcorn_amd.so`.
-The library is always rebuilt: the call is the "does it build" check. In a
-source tree it then writes the `popcorn-amd` distribution metadata beside the
-package (setup.py's `egg_info`, as an editable install would), so Popcorn's
-version gate sees the backend when the tree itself is on `sys.path`.
+The library is always rebuilt: the call is the "does it build" check. Asked
+to (`python -m popcorn_amd.build` and `__graft_entry__.build()` ask), it then
+writes the `popcorn-amd` distribution metadata beside the package in a source
+tree (setup.py's `egg_info`, as an editable install would), so Popcorn's
+version gate sees the backend when the tree itself is on `sys.path`. setup.py's
+own build step does not ask: an install writes its metadata itself.
 """
 
 from __future__ import annotations
@@ -61,8 +63,12 @@ def _compile(source: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile all kernels and link the shared library; returns its path."""
+def build(verbose: bool = False, write_metadata: bool = False) -> Path:
+    """Compile all kernels and link the shared library; returns its path.
+
+    With `write_metadata`, also write the distribution metadata into the source tree (see
+    `write_source_metadata`).
+    """
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
     workers = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16) or 1
@@ -76,11 +82,12 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
-    write_metadata()
+    if write_metadata:
+        write_source_metadata()
     return LIBRARY
 
 
-def write_metadata() -> None:
+def write_source_metadata() -> None:
     """Run setup.py's `egg_info` in a source tree (no-op for an installed package, which has its metadata)."""
     setup_py = PACKAGE.parent / "setup.py"
     if not setup_py.exists():
@@ -92,4 +99,4 @@ def write_metadata() -> None:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, write_metadata=True)

@@ -6,7 +6,12 @@ scalar args and which optional tensors are present -- with a stable 12-hex
 `Record` whose dictionary form is Popcorn's report-row schema 3
 (bench/model.py:105-163). The config layout, the id's hash payload and the row
 keys are a format shared with Popcorn: rows written here and rows Popcorn
-writes name the same cases and merge in either direction.
+writes name the same cases and load into each other's report files. Popcorn's
+selector still drops every row whose `ref_hash` / `impl_hash` differ from the
+fingerprints it computes itself (core/tuning.py:93-94, 127-128;
+core/fingerprint.py:163-202), and those of rows recorded here are this
+package's own, so such rows cannot steer upstream selection: rows meant for
+Popcorn's selector must be recorded by Popcorn itself.
 """
 
 from __future__ import annotations

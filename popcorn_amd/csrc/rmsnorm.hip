@@ -826,13 +826,16 @@ int pk_rmsnorm_bwd_noalloc(const void* x, const void* w, const float* rstd, cons
   const char* who = "pk_rmsnorm_bwd_noalloc";
   if (int st = check_shape(who, rows, cols, dtype, w_dtype)) return st;
   if (cols == 0) return fail(PK_ERR_INVALID, "%s: zero-width rows", who);
-  if (!x || !w || !rstd || !dy || !dx || !dw) return fail(PK_ERR_INVALID, "%s: null pointer", who);
   if (rows == 0) return fail(PK_ERR_UNSUPPORTED, "%s: zero rows (dw is all zeros; fill it host-side)", who);
+  // The size limit is checked before the pointers, so a caller can probe it
+  // with null pointers: a call past the limit then never reaches a launch,
+  // even if this check were wrong (the null check below refuses it).
   const int mode = dbias != nullptr ? kBias : kPlain;
   const int64_t need = workspace_layout(rows, cols, dtype, w_dtype, mode).total;
   if (need > kScratchBytes)
     return fail(PK_ERR_UNSUPPORTED, "%s: shape (%lld, %lld) needs %lld bytes of scratch, the fixed array holds %lld",
                 who, (long long)rows, (long long)cols, (long long)need, (long long)kScratchBytes);
+  if (!x || !w || !rstd || !dy || !dx || !dw) return fail(PK_ERR_INVALID, "%s: null pointer", who);
   void* base = nullptr;
   if (int st = scratch_address(who, &base)) return st;
   BwdArgs a{x, w, dy, nullptr, 0.f, rstd, dx, dw, dbias, nullptr, nullptr, nullptr, rows, (int)cols,

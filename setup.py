@@ -6,7 +6,8 @@
 Popcorn's version gate (core/sources.py:50-73) checks `importlib.metadata.version("popcorn-amd")`
 against the range `popcorn_amd.backend.register` declares, so the backend is eligible wherever
 this distribution's metadata is visible: after an install, or in the source tree once
-`popcorn_amd.build.build()` has written it there (it runs this file's `egg_info`).
+`python -m popcorn_amd.build` (or `__graft_entry__.build()`) has written it there (it runs this
+file's `egg_info`).
 """
 
 from __future__ import annotations

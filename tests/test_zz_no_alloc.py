@@ -122,12 +122,18 @@ def test_noalloc_other_dtypes_bias_and_row_widths(lib):
 
 
 def test_noalloc_refuses_a_shape_beyond_the_array(lib):
-    x, w, dy, _ = _inputs(4, 64, torch.float32, 0, False)
-    rstd = torch.ones(4, dtype=torch.float32, device=DEV)
-    dx, dw, db = torch.empty_like(x), torch.empty_like(w), torch.empty_like(w)
-    # 4096 rows of 2^18 fp32 columns: a partial row is 1 MiB, and the grid holds
-    # at least one block per CU (256), so 256 MiB of partials: refused before any launch.
-    rc = lib.pk_rmsnorm_bwd_noalloc(_ptr(x), _ptr(w), _ptr(rstd), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db),
-                                    4096, 1 << 18, _lib.F32, _lib.F32, _lib.stream_handle(torch.device(DEV)))
-    assert rc == _lib.ERR_UNSUPPORTED
+    # 4096 rows of 2^18 fp32 columns: a partial row is 1 MiB, and the grid holds at least one
+    # block per CU (256), so 256 MiB of partials against the 96 MiB array. The host-side layout
+    # says so first; the call then passes null pointers, so it can never launch: the entry point
+    # checks the size before the pointers, and were that check ever to regress, the null check
+    # would refuse the call with PK_ERR_INVALID instead of running out of bounds.
+    rows, cols = 4096, 1 << 18
+    assert lib.pk_rmsnorm_bwd_workspace(rows, cols, _lib.F32) > 96 << 20
+    rc = lib.pk_rmsnorm_bwd_noalloc(None, None, None, None, None, None, None, rows, cols, _lib.F32, _lib.F32,
+                                    _lib.stream_handle(torch.device(DEV)))
+    assert rc == _lib.ERR_UNSUPPORTED, lib.pk_last_error().decode()
     assert "scratch" in lib.pk_last_error().decode()
+    # within the limit, the same null pointers are refused as such (the order of the two checks)
+    rc = lib.pk_rmsnorm_bwd_noalloc(None, None, None, None, None, None, None, 64, 1024, _lib.F32, _lib.F32,
+                                    _lib.stream_handle(torch.device(DEV)))
+    assert rc == _lib.ERR_INVALID and "null pointer" in lib.pk_last_error().decode()
