@@ -227,7 +227,8 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
  * o like q; q head h reads kv head h / (q_heads / kv_heads). causal = 1 masks
  * key j > query i (top-left aligned). lse (fp32 [batch, q_heads, seq],
  * natural log) may be NULL. strides[12] = q, k, v, o (batch, seq, head)
- * strides in elements. dtype is PK_BF16 or PK_F16; head_dim 64 or 128.
+ * strides in elements. dtype is PK_BF16 or PK_F16; head_dim a multiple of 8
+ * up to 256 (rows laid out at 64, 128 or 256 dims, zeros past head_dim).
  * Replaces: reference `attn` (kernels/attn.py:10-37,
  * F.scaled_dot_product_attention with enable_gqa=True).
  */
@@ -272,7 +273,7 @@ int64_t pk_attn_bwd_workspace(int64_t batch, int64_t seq, int64_t q_heads, int64
  * head), dv = P^T dout; fp32 accumulation, one rounding per output, no atomics
  * (partials of q-head splits are added in a fixed order, so the result is
  * deterministic). strides[24] = q, k, v, o, dout, dq, dk, dv (batch, token,
- * head) strides in elements.
+ * head) strides in elements. head_dim a multiple of 8 up to 128.
  * Replaces torch autograd of the reference `attn` (kernels/attn.py:30-37).
  */
 int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,

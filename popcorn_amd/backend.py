@@ -136,12 +136,21 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
     )
 
 
+def _attn_head_dim(head_dim: int, *tensors: Any) -> bool:
+    """Rows of whole 16-byte chunks: head_dim a multiple of 8 up to 256 for the forward kernel, up to 128
+    when autograd must record the call (the backward kernels' widest rows)."""
+    if head_dim % 8 or not 8 <= head_dim <= 256:
+        return False
+    records = torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+    return head_dim <= 128 or not records
+
+
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:
     return (
         _on_hip(q, k, v)
         and q.dtype in (torch.bfloat16, torch.float16)
         and q.dtype == k.dtype == v.dtype
-        and q.shape[-1] in (64, 128)
+        and _attn_head_dim(q.shape[-1], q, k, v)
         and k.shape[2] > 0
         and q.shape[2] % k.shape[2] == 0
     )
@@ -156,7 +165,7 @@ def attn_varlen_supported(q, k, v, cu_seqlens, causal, softmax_scale) -> bool:
         and q.dtype in (torch.bfloat16, torch.float16)
         and q.dtype == k.dtype == v.dtype
         and q.dim() == 3
-        and q.shape[-1] in (64, 128)
+        and _attn_head_dim(q.shape[-1], q, k, v)
         and k.shape[1] > 0
         and q.shape[1] % k.shape[1] == 0
     )

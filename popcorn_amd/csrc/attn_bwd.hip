@@ -94,7 +94,15 @@ struct BwdArgs {
   float scale;  // signed softmax scale
   float c;      // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;
+  // head_dim of the tensors (a multiple of 8, at most the kernels' D) and its
+  // 16-byte chunks: rows are laid out at D, reading zeros past head_dim
+  int dr, dch;
 };
+
+// Buffer offset of a chunk past head_dim: at or past every range the kernels
+// build (each below 2^31), and with a tile offset below 2^31 added it cannot
+// wrap, so the load returns zeros without a memory access.
+constexpr uint32_t kPadOffset = 0x80000000u;
 
 // LDS tile layout: unpadded rows, 16-byte chunk c of row r at c ^ swz(r)
 template <int D> struct Tile {
@@ -179,8 +187,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const T* gbase = static_cast<const T*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
   const T* kbase = static_cast<const T*>(a.k) + b * a.ks[0] + hkv * a.ks[2] + start * a.ks[1];
   const T* vbase = static_cast<const T*>(a.v) + b * a.vs[0] + hkv * a.vs[2] + start * a.vs[1];
-  const int k_bytes = (int)(((int64_t)(S - 1) * a.ks[1] + D) * (int)sizeof(T));
-  const int v_bytes = (int)(((int64_t)(S - 1) * a.vs[1] + D) * (int)sizeof(T));
+  const int k_bytes = (int)(((int64_t)(S - 1) * a.ks[1] + a.dr) * (int)sizeof(T));
+  const int v_bytes = (int)(((int64_t)(S - 1) * a.vs[1] + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
 
@@ -190,7 +198,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
     uint4 qr = make_uint4(0, 0, 0, 0), gr = qr, orr = qr;
-    if (row_ok) {
+    if (row_ok && 2 * kk + g < a.dch) {
       const int64_t col = 16 * kk + 8 * g;
       qr = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qs[1] + col);
       gr = *reinterpret_cast<const uint4*>(gbase + (int64_t)q_row * a.gs[1] + col);
@@ -220,8 +228,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
     const int sl = i * NT + tid, row = sl / KCH, c = (sl % KCH) ^ L::swz(row);
-    kgo[i] = (row * (int)a.ks[1] + c * 8) * (int)sizeof(T);
-    vgo[i] = (row * (int)a.vs[1] + c * 8) * (int)sizeof(T);
+    kgo[i] = c < a.dch ? (row * (int)a.ks[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
+    vgo[i] = c < a.dch ? (row * (int)a.vs[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   auto issue = [&](int t, int buf) {
 #pragma unroll
@@ -371,8 +379,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
-        *reinterpret_cast<uint2*>(drow + dt * 32 + 8 * rq + 4 * g) =
-            pack4<T>(acc[dt][4 * rq] * a.scale, acc[dt][4 * rq + 1] * a.scale, acc[dt][4 * rq + 2] * a.scale,
+        if (dt * 32 + 8 * rq + 4 * g < a.dr)
+          *reinterpret_cast<uint2*>(drow + dt * 32 + 8 * rq + 4 * g) =
+              pack4<T>(acc[dt][4 * rq] * a.scale, acc[dt][4 * rq + 1] * a.scale, acc[dt][4 * rq + 2] * a.scale,
                      acc[dt][4 * rq + 3] * a.scale);
   }
 }
@@ -444,7 +453,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       uint4 r = make_uint4(0, 0, 0, 0);
-      if (key_ok) r = *reinterpret_cast<const uint4*>(row + 16 * kk + 8 * g);
+      if (key_ok && 2 * kk + g < a.dch) r = *reinterpret_cast<const uint4*>(row + 16 * kk + 8 * g);
       bf[kk] = __builtin_bit_cast(Frag, r);
     }
   }
@@ -465,7 +474,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   for (int i = 0; i < TI; ++i) {
     const int sl = i * NT2 + tid, op = sl / SLOTS, within = sl % SLOTS;
     const int row = within / KCH, c = (within % KCH) ^ L::swz(row);
-    go[i] = (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T);
+    go[i] = c < a.dch ? (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   // Tiles are issued in order: a cursor holds the next tile's q head (within
   // the group) and q tile, and the buffer descriptors of that head, rebuilt
@@ -485,7 +494,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       const bool isq = i * NT2 + wave * 64 < SLOTS;  // wave-uniform
       tstride[i] = (int)(isq ? a.qs[1] : a.gs[1]) * (int)sizeof(T);
       trs[i] = __builtin_amdgcn_make_buffer_rsrc((void*)(isq ? qb : gb), (short)0,
-                                                 (int)(((int64_t)(S - 1) * (isq ? a.qs[1] : a.gs[1]) + D) * (int)sizeof(T)),
+                                                 (int)(((int64_t)(S - 1) * (isq ? a.qs[1] : a.gs[1]) + a.dr) * (int)sizeof(T)),
                                                  0x00020000);
     }
     rrs = __builtin_amdgcn_make_buffer_rsrc((void*)(wave == 0 ? db + a.lse_n : db), (short)0, S * (int)sizeof(float),
@@ -698,7 +707,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq)
-          *reinterpret_cast<float4*>(out + dt * 32 + 8 * rq + 4 * g) =
+          if (dt * 32 + 8 * rq + 4 * g < a.dr)
+            *reinterpret_cast<float4*>(out + dt * 32 + 8 * rq + 4 * g) =
               make_float4(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
     } else {
       T* out = role == 0
@@ -708,8 +718,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq)
-          *reinterpret_cast<uint2*>(out + dt * 32 + 8 * rq + 4 * g) =
-              pack4<T>(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
+          if (dt * 32 + 8 * rq + 4 * g < a.dr)
+            *reinterpret_cast<uint2*>(out + dt * 32 + 8 * rq + 4 * g) =
+                pack4<T>(acc[dt][4 * rq] * f, acc[dt][4 * rq + 1] * f, acc[dt][4 * rq + 2] * f, acc[dt][4 * rq + 3] * f);
     }
   }
 }
@@ -719,12 +730,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
 // (dense) or the packed token index.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void dkdv_sum_kernel(BwdArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over rows * Hkv * D / 4
-  const int64_t n = a.rows * a.Hkv * (D / 4);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over rows * Hkv * head_dim / 4
+  const int q4 = a.dr / 4;
+  const int64_t n = a.rows * a.Hkv * q4;
   if (i >= n) return;
-  const int d4 = (int)(i % (D / 4)) * 4;
-  const int hkv = (int)((i / (D / 4)) % a.Hkv);
-  const int64_t row = i / ((int64_t)(D / 4) * a.Hkv);
+  const int d4 = (int)(i % q4) * 4;
+  const int hkv = (int)((i / q4) % a.Hkv);
+  const int64_t row = i / ((int64_t)q4 * a.Hkv);
   const int64_t b = a.cu != nullptr ? 0 : row / a.S;
   const int64_t t = a.cu != nullptr ? row : row % a.S;
   const int64_t stride = a.rows * a.Hkv * D;  // one (split, role) slab
@@ -758,7 +770,7 @@ int launch(const BwdArgs& a, bool causal, hipStream_t s) {
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   }
   if (a.nsplit > 1) {
-    const int64_t n = a.rows * a.Hkv * (D / 4);
+    const int64_t n = a.rows * a.Hkv * (a.dr / 4);
     hipLaunchKernelGGL((dkdv_sum_kernel<T, D>), dim3((n + 255) / 256), dim3(256), 0, s, a);
   }
   return launched("pk_attn_bwd");
@@ -780,8 +792,10 @@ inline int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; 
 
 // Workspace bytes: D and lse2 (2 * lse_n floats), then the dk/dv partials when
 // the kernel splits the q heads.
+// (The partials are laid out at the kernels' row width: 64 or 128 dims.)
 int64_t workspace_bytes(int64_t lse_n, int64_t rows, int64_t kv_heads, int64_t head_dim, int nsplit) {
-  const int64_t parts = nsplit > 1 ? (int64_t)nsplit * 2 * rows * kv_heads * head_dim * (int64_t)sizeof(float) : 0;
+  const int64_t width = head_dim <= 64 ? 64 : 128;
+  const int64_t parts = nsplit > 1 ? (int64_t)nsplit * 2 * rows * kv_heads * width * (int64_t)sizeof(float) : 0;
   return round_up(2 * lse_n * (int64_t)sizeof(float)) + parts;
 }
 
@@ -806,8 +820,8 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.dsum = static_cast<float*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(2 * a.lse_n * (int64_t)sizeof(float)));
   if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
-  if (head_dim != 64 && head_dim != 128)
-    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (64 or 128 only)", who, (long long)head_dim);
+  if (head_dim <= 0 || head_dim > 128 || head_dim % 8 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to 128)", who, (long long)head_dim);
   if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
   if (seq > (1 << 30) || batch * q_heads > (1 << 20)) return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
   const void* ptrs[] = {a.q, a.k, a.v, a.o, a.dout, a.dq, a.dk, a.dv};
@@ -833,10 +847,13 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.scale = softmax_scale;
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
+  a.dr = (int)head_dim;
+  a.dch = (int)(head_dim / 8);
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PK_BF16) return head_dim == 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
-  return head_dim == 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
+  // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
+  if (dtype == PK_BF16) return head_dim <= 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
+  return head_dim <= 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
 }
 
 }  // namespace

@@ -76,7 +76,9 @@ using namespace attn;
 
 constexpr int BN = 32;
 constexpr int NT = 256;
-constexpr int kRing = 6;  // fragment reads in flight ahead of the product that uses them
+// fragment reads in flight ahead of the product that uses them (head_dim 256,
+// whose Q^T fragments and O^T accumulators take 192 registers, keeps fewer)
+template <int D> constexpr int kRing = D == 256 ? 3 : 6;
 // Buffer offset of a padding slot: at or past every range the kernel builds
 // (each below 2^31), and with a tile offset below 2^31 added it cannot wrap.
 constexpr uint32_t kPadOffset = 0x80000000u;
@@ -84,7 +86,7 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 // Slot of chunk c of V row r is c ^ vswz(r): the two 16-lane groups of a
 // transposing read cover 4 rows x 4 chunks, which this spreads over 16
 // distinct slots of a 256-byte bank window (rows of head_dim 64 are 128 bytes).
-template <int D> __device__ __forceinline__ int vswz(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+template <int D> __device__ __forceinline__ int vswz(int r) { return D >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 
 // Largest row sum the fixed-max sweep accepts (see the header).
 template <typename T> constexpr float kFastLimit = 4294967296.0f;
@@ -106,6 +108,9 @@ struct AttnArgs {
   int gp;  // q heads of one kv group per block (4, 2 or 1); the block's 4 waves are gp heads x 4/gp row groups
   float c;          // |scale| * log2(e), at least 1e-30
   uint32_t q_flip;  // 0x80008000 when scale < 0 (negates both halves of a packed pair), else 0
+  // head_dim of the tensors (a multiple of 8, at most the kernel's D) and its
+  // 16-byte chunks: the kernel lays rows out at D and reads zeros past them
+  int dr, dch;
 };
 
 template <typename T, int D, bool CAUSAL>
@@ -170,8 +175,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const T* vbase = static_cast<const T*>(a.v) + b * a.vsb + hkv * a.vsh + start * a.vss;
   // K/V of this (sequence, kv head) through buffer resources: rows at or past
   // S read as zero (range-checked), and a tile's base is one scalar offset.
-  const int k_bytes = (int)(((int64_t)(S - 1) * a.kss + D) * (int)sizeof(T));
-  const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + D) * (int)sizeof(T));
+  const int k_bytes = (int)(((int64_t)(S - 1) * a.kss + a.dr) * (int)sizeof(T));
+  const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
 
@@ -180,7 +185,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk) {
     uint4 raw = make_uint4(0, 0, 0, 0);
-    if (q_row < S) raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
+    if (q_row < S && 2 * kk + g < a.dch)
+      raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
     raw.x ^= a.q_flip;
     raw.y ^= a.q_flip;
     raw.z ^= a.q_flip;
@@ -202,7 +208,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
     const int sl = i * NT + tid, row = sl / KSPR, col = sl % KSPR;
-    kgo[i] = col < KCH ? (row * (int)a.kss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
+    kgo[i] = col < a.dch ? (row * (int)a.kss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   // V rows are unpadded, chunk c of row r at slot c ^ vswz(r); the rows of one
   // instruction's slots differ from the next's by NT / KCH (a multiple of 4),
@@ -211,8 +217,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   static_assert(BN * KCH % NT == 0 && (NT / KCH) % 4 == 0, "V staging covers whole rows");
   int vgo;
   {
-    const int row = tid / KCH, pos = tid % KCH;
-    vgo = (row * (int)a.vss + (pos ^ vswz<D>(row)) * 8) * (int)sizeof(T);
+    const int row = tid / KCH, pos = tid % KCH, chunk = pos ^ vswz<D>(row);
+    vgo = chunk < a.dch ? (row * (int)a.vss + chunk * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
   // dims 16kk + 8g ..), and the transposing V reads (see pv)
@@ -342,13 +348,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
       return *reinterpret_cast<const Frag*>(ks + 16 * (i - KK));
     };
     constexpr int N = 2 * KK;  // 2 * DT == KK products of each kind
-    Frag ring[kRing];
+    Frag ring[kRing<D>];
 #pragma unroll
-    for (int i = 0; i < kRing; ++i) ring[i] = fetch(i);
+    for (int i = 0; i < kRing<D>; ++i) ring[i] = fetch(i);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const Frag f = ring[i % kRing];
-      if (i + kRing < N) ring[i % kRing] = fetch(i + kRing);
+      const Frag f = ring[i % kRing<D>];
+      if (i + kRing<D> < N) ring[i % kRing<D>] = fetch(i + kRing<D>);
       if (i < KK) {
         acc[i % DT] = Mma<T>::run(f, pf[i / DT], acc[i % DT]);
       } else {
@@ -420,6 +426,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d0 = dt * 32 + 8 * rq + 4 * g;
+        if (d0 >= a.dr) continue;
         const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq] * inv)) |
                             ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq + 1] * inv)) << 16);
         const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(acc[dt][4 * rq + 2] * inv)) |
@@ -460,8 +467,8 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
     return fail(PK_ERR_INVALID, "%s: q_heads=%lld is not a multiple of kv_heads=%lld", who, (long long)q_heads,
                 (long long)kv_heads);
   if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
-  if (head_dim != 64 && head_dim != 128)
-    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (64 or 128 only)", who, (long long)head_dim);
+  if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to 256)", who, (long long)head_dim);
   if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
   if (seq > (1 << 30) || batch * q_heads > (1 << 20)) return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.o))
@@ -496,10 +503,16 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   if (reach > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: K/V rows span more than 2 GiB per head", who);
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
+  a.dr = (int)head_dim;
+  a.dch = (int)(head_dim / 8);
   if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == PK_BF16) return head_dim == 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
-  return head_dim == 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
+  // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
+  if (dtype == PK_BF16)
+    return head_dim <= 64 ? launch<bf16, 64>(a, causal, s)
+                          : head_dim <= 128 ? launch<bf16, 128>(a, causal, s) : launch<bf16, 256>(a, causal, s);
+  return head_dim <= 64 ? launch<f16, 64>(a, causal, s)
+                        : head_dim <= 128 ? launch<f16, 128>(a, causal, s) : launch<f16, 256>(a, causal, s);
 }
 
 }  // namespace

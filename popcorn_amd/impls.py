@@ -620,12 +620,19 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
     """softmax(q k^T * scale + causal mask) v with grouped kv heads.
 
     q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim];
-    bf16 or fp16; head_dim 64 or 128; scale defaults to head_dim ** -0.5.
-    Backward gives dq, dk, dv.
+    bf16 or fp16; head_dim a multiple of 8 up to 256 (up to 128 with
+    gradients); scale defaults to head_dim ** -0.5. Backward gives dq, dk, dv.
     """
     if _tracks_grad(q, k, v):
+        _grad_head_dim("attn", q.shape[-1])
         return _Attention.apply(q, k, v, causal, softmax_scale)
     return _attn_fwd(q, k, v, causal, softmax_scale, want_lse=False)[0]
+
+
+def _grad_head_dim(op: str, head_dim: int) -> None:
+    """Refuse, before any work, a call whose backward the kernels do not cover."""
+    if head_dim > 128:
+        raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} has a forward kernel only (gradients up to 128)")
 
 
 def _scale(head_dim: int, softmax_scale: float | None) -> float:
@@ -717,11 +724,12 @@ def attn_varlen(
 
     q [total, q_heads, head_dim], k, v [total, kv_heads, head_dim]; cu_seqlens
     int32 [num_seqs + 1] offsets from 0 to total (the flash-attention varlen
-    layout). Causal masks are top-left aligned within each sequence. Backward
-    gives dq, dk, dv.
+    layout). Causal masks are top-left aligned within each sequence. head_dim
+    as for `attn`. Backward gives dq, dk, dv.
     """
     cu, num_seqs, longest = _cut_points(cu_seqlens, q.shape[0], q.device)
     if _tracks_grad(q, k, v):
+        _grad_head_dim("attn_varlen", q.shape[-1])
         return _AttentionVarlen.apply(q, k, v, cu, num_seqs, longest, causal, softmax_scale)
     return _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=False)[0]
 

@@ -77,3 +77,37 @@ def test_predicates_cover_the_mixed_dtype_pairs(monkeypatch):
     assert not backend.qk_norm_rope_supported(q, k, w32, t(64, dtype=bf), c32, c32, 1e-6)
     q32, k32 = t(2, 4, 8, 64, dtype=f32), t(2, 2, 8, 64, dtype=f32)
     assert not backend.qk_norm_rope_supported(q32, k32, t(64, dtype=bf), t(64, dtype=bf), c32, c32, 1e-6)
+
+
+def test_attention_predicates_cover_the_head_dims(monkeypatch):
+    """Forward at every head_dim that is a multiple of 8 up to 256 (Popcorn's grid, core/dims.py:74);
+    with gradients to record up to 128, the backward kernels' widest rows; other widths declined."""
+    monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
+
+    def qkv(d, grad=False):
+        q = torch.empty(1, 16, 8, d, dtype=torch.bfloat16, device="meta")
+        k = torch.empty(1, 16, 2, d, dtype=torch.bfloat16, device="meta")
+        return [t.requires_grad_(grad) for t in (q, k, k.clone())]
+
+    for d in (16, 32, 48, 64, 80, 96, 128, 192, 256):
+        assert backend.attn_supported(*qkv(d), True, None)
+        assert backend.attn_supported(*qkv(d, grad=True), True, None) == (d <= 128)
+        with torch.no_grad():  # nothing recorded: the forward kernel serves any of them
+            assert backend.attn_supported(*qkv(d, grad=True), True, None)
+    for d in (8 * 33, 72 + 4, 100, 4):
+        assert not backend.attn_supported(*qkv(d), True, None)
+    q, k, v = (t[0] for t in qkv(96))
+    assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), True, None)
+
+
+def test_attention_with_gradients_past_head_dim_128_is_refused_before_any_work():
+    from popcorn_amd import impls
+
+    q = torch.randn(1, 4, 2, 192, requires_grad=True)  # CPU tensors: the refusal comes first
+    for call in (lambda: impls.attn(q, q, q, True), lambda: impls.attn_varlen(q[0], q[0], q[0], torch.tensor([0, 4]))):
+        try:
+            call()
+        except ValueError as e:
+            assert "forward kernel only" in str(e)
+        else:
+            raise AssertionError("head_dim 192 with gradients was not refused")
