@@ -80,6 +80,8 @@ class Workload:
     # every kernel one `launch` runs, when it is more than the dominant one (the launch's time then
     # covers them all, so the achieved rate of the dominant kernel is understated, never overstated)
     launch_kernels: tuple[str, ...] = ()
+    # figures the workload reports beside its rate, read after the timed calls
+    extra: Callable[[], dict] | None = None
 
 
 def _copies(nbytes: int) -> int:
@@ -91,7 +93,7 @@ def _randn(shape, dtype, gen, dev):
     return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).to(dtype)
 
 
-def make_workload(name: str, dev: torch.device) -> Workload:
+def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload:
     from popcorn_amd import _lib, impls
     from popcorn_amd.compat import references as R
 
@@ -417,7 +419,7 @@ def make_workload(name: str, dev: torch.device) -> Workload:
 
     if name == "attn_bwd":
         # not a BASELINE config: attention forward + backward at C5's shape (bf16, causal)
-        B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
+        B, S, HQ, HKV, D = 4, 8192, 32, 8, head_dim
         q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
         k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
         v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
@@ -458,14 +460,15 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             out = R.attn(qg, kg, vg, True)
             torch.autograd.grad(out, (qg, kg, vg), do)
 
-        return Workload("attn_bwd", "Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16",
+        return Workload("attn_bwd" if D == 128 else f"attn_bwd_d{D}",
+                        f"Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D={D}", "bf16",
                         "TFLOP/s", fwd_flops + bwd_flops, step, "attn_bwd", bwd_flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
                          "dtype": "bf16"}, cpu, torch_step,
                         launch_kernels=("attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"))
 
     if name == "c5":
-        B, S, HQ, HKV, D = 4, 8192, 32, 8, 128
+        B, S, HQ, HKV, D = 4, 8192, 32, 8, head_dim
         q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
         k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
         v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
@@ -508,10 +511,34 @@ def make_workload(name: str, dev: torch.device) -> Workload:
             with torch.no_grad():
                 R.attn(q, k, v, True)
 
-        return Workload("c5", "Causal GQA attention fwd bf16 B=4 S=8192 Hq=32 Hkv=8 D=128", "bf16", "TFLOP/s",
+        return Workload("c5" if D == 128 else f"c5_d{D}", f"Causal GQA attention fwd bf16 B=4 S=8192 Hq=32 Hkv=8 D={D}",
+                        "bf16", "TFLOP/s",
                         flops, step, "attn_fwd_kernel", flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
                          "dtype": "bf16"}, cpu, torch_step)
+
+    if name in ("mfma_ceiling", "mfma_ceiling_softmax"):
+        # not a BASELINE config: the matrix-core rate this board sustains under its power limit,
+        # random bf16 operands toggling like real data (pk_probe_mfma), one wave per SIMD on every CU
+        softmax = int(name.endswith("softmax"))
+        blocks = torch.cuda.get_device_properties(dev).multi_processor_count
+        iters = 2048  # 2048 x 8 products of 32 cycles: about 0.3 ms per launch at 1.8 GHz
+        out = torch.zeros(2 * 4 * blocks, dtype=torch.int64, device=dev)
+        flops = 4.0 * blocks * iters * 8 * (2 * 32 * 32 * 16)
+
+        def step(i):
+            _lib.check(lib.pk_probe_mfma(softmax, iters, blocks, out.data_ptr(), stream()))
+
+        def extra():
+            cycles, ticks = out.view(-1, 2).double().cpu().unbind(1)
+            return {"cycles_per_product": round(float(cycles.mean()) / (iters * 8), 3),
+                    "clock_mhz": round(float((cycles / ticks).mean()) * 100.0, 1)}  # ticks run at 100 MHz
+
+        what = "bf16 32x32x16 products" + (" with the attention forward's per-score vector work" if softmax else "")
+        return Workload(name, f"matrix-core probe: {what}, {blocks} CUs x 4 waves", "bf16", "TFLOP/s", flops, step,
+                        "mfma_probe_kernel", flops, step,
+                        {"blocks": blocks, "waves_per_simd": 1, "products_per_wave": iters * 8,
+                         "softmax": bool(softmax)}, extra=extra)
 
     if name == "copy":
         numel = 256 << 20  # 512 MiB of bf16 each way
@@ -525,7 +552,47 @@ def make_workload(name: str, dev: torch.device) -> Workload:
         return Workload("copy", "plain device copy, 512 MiB -> 512 MiB", "bf16", "TB/s", nbytes, step, "copy",
                         nbytes, step, {"bytes_each_way": numel * 2})
 
-    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, attn_bwd, copy)")
+    raise SystemExit(f"bench.py: unknown workload {name!r} (c1..c5, add_rmsnorm, rope, qk_norm_rope, attn_bwd, "
+                     "mfma_ceiling, mfma_ceiling_softmax, copy)")
+
+
+def _amd_smi_power() -> dict | None:
+    """One `amd-smi metric -p -c` sample of GPU 0: socket power and the graphics clock of each XCD."""
+    import re
+    import subprocess
+    try:
+        text = subprocess.run(["amd-smi", "metric", "-p", "-c", "-g", "0"], capture_output=True, text=True,
+                              timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    power = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", text)
+    clocks = [int(m) for m in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([0-9]+)\s*MHz", text)]
+    if power is None and not clocks:
+        return None
+    return {"socket_power_w": float(power.group(1)) if power else None, "gfx_clock_mhz": clocks}
+
+
+def _power_sample(fn: Callable[[int], None], seconds: float) -> dict | None:
+    """Run `fn` back to back for `seconds` and sample board power and clocks two thirds of the way in.
+
+    The sample comes from `amd-smi` in a thread while the calls keep the GPU busy; the clock it
+    reports is what the power manager allows this workload.
+    """
+    import threading
+    box: dict = {}
+    sampler = threading.Timer(seconds * 2 / 3, lambda: box.update(sample=_amd_smi_power()))
+    calls, t0 = 0, time.perf_counter()
+    sampler.start()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn(calls)
+            calls += 1
+        torch.cuda.synchronize()
+    sampler.join()
+    sample = box.get("sample")
+    if sample is None:
+        return None
+    return {**sample, "seconds": seconds, "calls": calls, "ms_per_call": round((time.perf_counter() - t0) * 1e3 / calls, 4)}
 
 
 def _time_cpu(fn, budget_s: float = 5.0, min_reps: int = 2, max_reps: int = 20) -> tuple[float, int]:
@@ -635,8 +702,12 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope",
-                                                           "qk_norm_rope",
-                                                           "attn_bwd", "copy"])
+                                                           "qk_norm_rope", "attn_bwd", "mfma_ceiling",
+                                                           "mfma_ceiling_softmax", "copy"])
+    ap.add_argument("--head-dim", type=int, default=128,
+                    help="head_dim of the c5 and attn_bwd workloads (128 is the BASELINE config)")
+    ap.add_argument("--power", action="store_true",
+                    help="also run the workload for a few seconds and report amd-smi socket power and clocks")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-others", action="store_true", help="skip the other configs' kernel figures")
     args = ap.parse_args(argv)
@@ -652,7 +723,7 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
 
     print(f"bench: workload {args.workload}, {args.warmup} warmup + {args.steps} steps", file=sys.stderr, flush=True)
-    wl = make_workload(args.workload, dev)
+    wl = make_workload(args.workload, dev, args.head_dim)
     torch.cuda.synchronize()
     total_ms = _time_gpu(wl.step, args.steps, args.warmup)
     ms_per_step = total_ms / args.steps
@@ -661,13 +732,17 @@ def main(argv=None) -> int:
     roof = _roofline(wl, args.steps, args.warmup)
     print(f"bench: {wl.kernel} {roof['avg_launch_us']} us/launch, frac {roof['frac']}", file=sys.stderr, flush=True)
 
+    extra = wl.extra() if wl.extra is not None else None
+    power = _power_sample(wl.step, 6.0) if args.power else None
+    if power:
+        print(f"bench: power {power}", file=sys.stderr, flush=True)
     torch_gpu = _torch_on_gpu(wl, ms_per_step, args.steps, args.warmup)
     if torch_gpu:
         print(f"bench: torch on the GPU {torch_gpu['ms_per_step']} ms/step ({torch_gpu['speedup']}x)", file=sys.stderr,
               flush=True)
     head_unit, head_dtype, head_config = wl.unit, wl.dtype, {"workload": wl.description, **wl.config}
     others = {}
-    if not args.no_others and wl.name != "copy":
+    if not args.no_others and args.workload not in ("copy", "mfma_ceiling", "mfma_ceiling_softmax"):
         del wl
         for name in ("c1", "c2", "c3", "c4", "c5", "attn_bwd", "add_rmsnorm", "rope", "qk_norm_rope"):
             if name == args.workload:
@@ -697,7 +772,7 @@ def main(argv=None) -> int:
     if not args.no_cpu:
         for name in (args.workload, *others):
             torch.cuda.empty_cache()
-            wl_c = make_workload(name, dev)
+            wl_c = make_workload(name, dev, args.head_dim if name == args.workload else 128)
             result = _cpu_baseline(wl_c)
             if name == args.workload:
                 cpu = result
@@ -727,6 +802,10 @@ def main(argv=None) -> int:
         "roofline_fractions": {name: fractions[name] for name in ("c1", "c2", "c3", "c4", "c5") if name in fractions},
         "others": others,
     }
+    if extra is not None:
+        line["probe"] = extra
+    if power is not None:
+        line["power"] = power
     print(json.dumps(line), flush=True)
     return 0
 

@@ -301,6 +301,17 @@ int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* 
                        const int64_t* strides, int64_t num_seqs, int64_t total, int64_t max_seqlen, int64_t q_heads,
                        int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream);
 
+/*
+ * Matrix-core rate probe, a measurement aid with no counterpart in the
+ * reference: `blocks` blocks of four waves (one per SIMD; pass the CU count to
+ * fill the device) each run iters x 8 back-to-back bf16 32x32x16 products on
+ * random operands, with (softmax != 0) or without the attention forward's
+ * per-score vector work beside each product. out (device, uint64
+ * [2 * 4 * blocks]) receives per wave the shader-clock cycles and the 100 MHz
+ * real-time ticks of its loop. Reads no memory.
+ */
+int pk_probe_mfma(int softmax, int iters, int blocks, uint64_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
