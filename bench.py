@@ -540,6 +540,32 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
                         {"blocks": blocks, "waves_per_simd": 1, "products_per_wave": iters * 8,
                          "softmax": bool(softmax)}, extra=extra)
 
+    if name.startswith("stream_"):
+        # not a BASELINE config: the streaming ceiling at a config's pattern and size, e.g. stream_1r_64m
+        # (C1: one read and one write of 64 MiB) or stream_2r_160m (qk_norm_rope's backward: two reads
+        # and one write of 160 MiB); pk_probe_stream, inputs and outputs rotated like C1's
+        try:
+            reads, mib = name[len("stream_"):].split("_")
+            reads, nbytes = int(reads.rstrip("r")), int(mib.rstrip("m")) << 20
+        except ValueError:
+            raise SystemExit(f"bench.py: stream workload {name!r} is not stream_<1|2>r_<MiB>m")
+        if reads not in (1, 2) or nbytes <= 0:
+            raise SystemExit(f"bench.py: stream workload {name!r} is not stream_<1|2>r_<MiB>m")
+        n = _copies(reads * nbytes)
+        ins = [[torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(generator=gen) for _ in range(reads)]
+               for _ in range(n)]
+        outs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
+        moved = (reads + 1) * nbytes
+
+        def step(i):
+            a = ins[i % n]
+            _lib.check(lib.pk_probe_stream(a[0].data_ptr(), a[-1].data_ptr() if reads == 2 else None,
+                                           outs[i % n].data_ptr(), nbytes, reads, stream()))
+
+        return Workload(name, f"streaming probe: {reads} read(s) + 1 write of {nbytes >> 20} MiB each, {n} copies "
+                        "rotated", "u8", "TB/s", moved, step, "stream_probe_kernel", moved, step,
+                        {"reads": reads, "bytes_each": nbytes, "copies": n})
+
     if name == "copy":
         numel = 256 << 20  # 512 MiB of bf16 each way
         src = torch.empty(numel, dtype=torch.bfloat16, device=dev).fill_(1.0)
@@ -701,9 +727,16 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope",
-                                                           "qk_norm_rope", "attn_bwd", "mfma_ceiling",
-                                                           "mfma_ceiling_softmax", "copy"])
+    named = ["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope", "attn_bwd", "mfma_ceiling",
+             "mfma_ceiling_softmax", "copy"]
+
+    def workload_name(text: str) -> str:
+        if text in named or text.startswith("stream_"):
+            return text
+        raise argparse.ArgumentTypeError(f"{text!r} is none of {', '.join(named)} or stream_<1|2>r_<MiB>m")
+
+    ap.add_argument("--workload", default="c2", type=workload_name,
+                    help=f"one of {', '.join(named)}, or stream_<1|2>r_<MiB>m (the streaming ceiling)")
     ap.add_argument("--head-dim", type=int, default=128,
                     help="head_dim of the c5 and attn_bwd workloads (128 is the BASELINE config)")
     ap.add_argument("--power", action="store_true",
@@ -742,7 +775,8 @@ def main(argv=None) -> int:
               flush=True)
     head_unit, head_dtype, head_config = wl.unit, wl.dtype, {"workload": wl.description, **wl.config}
     others = {}
-    if not args.no_others and args.workload not in ("copy", "mfma_ceiling", "mfma_ceiling_softmax"):
+    if not args.no_others and args.workload in ("c1", "c2", "c3", "c4", "c5", "attn_bwd", "add_rmsnorm", "rope",
+                                                 "qk_norm_rope"):
         del wl
         for name in ("c1", "c2", "c3", "c4", "c5", "attn_bwd", "add_rmsnorm", "rope", "qk_norm_rope"):
             if name == args.workload:

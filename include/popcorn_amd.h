@@ -312,6 +312,15 @@ int pk_attn_varlen_bwd(const void* q, const void* k, const void* v, const void* 
  */
 int pk_probe_mfma(int softmax, int iters, int blocks, uint64_t* out, void* stream);
 
+/*
+ * Streaming probe, the HBM counterpart of pk_probe_mfma (no counterpart in the
+ * reference): y = a (reads == 1) or y = a ^ b (reads == 2) over `bytes` bytes
+ * (a multiple of 16, 16-byte aligned pointers), one 16-byte non-temporal
+ * vector per thread in 64-thread blocks: the ceiling of a streaming kernel
+ * with that pattern of reads and writes at that size.
+ */
+int pk_probe_stream(const void* a, const void* b, void* y, int64_t bytes, int reads, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ SIGNATURES = {
     "pk_attn_varlen_bwd": (_int, [_p] * 7 + [_i64] + [_p] * 5 + [_i64] * 6 + [_f32, _int, _int, _p]),
     "pk_attn_varlen_fwd": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _p]),
     "pk_probe_mfma": (_int, [_int, _int, _int, _p, _p]),
+    "pk_probe_stream": (_int, [_p, _p, _p, _i64, _int, _p]),
 }
 
 _lock = threading.Lock()

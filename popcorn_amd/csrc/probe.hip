@@ -12,7 +12,13 @@
 // 2.4 GHz peak clock). No counterpart in Popcorn: a measurement aid for the
 // bench, not an operator.
 //
-// Registers are named in the assembly: fragments in v200-v231, the vector
+// The streaming probe is the HBM counterpart: the fastest stream form found
+// for these kernels (one 16-byte non-temporal vector per thread, 64-thread
+// blocks, one vector per thread in all) copying one input or combining two,
+// which gives the ceiling that a streaming kernel with the same reads and
+// writes per byte can reach at a given size.
+//
+// Registers of the matrix-core probe are named in the assembly: fragments in v200-v231, the vector
 // work in v232-v238, accumulators in a0-a127, all declared clobbered, so the
 // compiler keeps nothing of its own there. Nothing is read from memory; the
 // only store is the per-wave timing pair.
@@ -280,10 +286,44 @@ void mfma_probe_kernel(uint64_t* out, int iters) {
   }
 }
 
+constexpr int kStreamThreads = 64;
+
+// y = a (one read) or y = a ^ b (two reads), one 16-byte vector per thread
+template <bool TWO>
+__global__ __launch_bounds__(kStreamThreads) void stream_probe_kernel(const u32x4* a, const u32x4* b, u32x4* y,
+                                                                      int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
+  if (i >= n) return;
+  u32x4 v = __builtin_nontemporal_load(a + i);
+  if constexpr (TWO) v ^= __builtin_nontemporal_load(b + i);
+  __builtin_nontemporal_store(v, y + i);
+}
+
 }  // namespace
 }  // namespace pk
 
 extern "C" {
+
+int pk_probe_stream(const void* a, const void* b, void* y, int64_t bytes, int reads, void* stream) {
+  using namespace pk;
+  if (reads != 1 && reads != 2) return fail(PK_ERR_INVALID, "pk_probe_stream: reads %d is neither 1 nor 2", reads);
+  if (bytes < 0 || bytes % 16) return fail(PK_ERR_INVALID, "pk_probe_stream: %lld bytes is not a multiple of 16",
+                                            (long long)bytes);
+  if (bytes == 0) return PK_OK;
+  if (!a || !y || (reads == 2 && !b)) return fail(PK_ERR_INVALID, "pk_probe_stream: null pointer");
+  if (!aligned16(a) || !aligned16(y) || (reads == 2 && !aligned16(b)))
+    return fail(PK_ERR_INVALID, "pk_probe_stream: pointers must be 16-byte aligned");
+  const int64_t n = bytes / 16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((n + kStreamThreads - 1) / kStreamThreads));
+  if (reads == 2)
+    hipLaunchKernelGGL(stream_probe_kernel<true>, grid, dim3(kStreamThreads), 0, s, static_cast<const u32x4*>(a),
+                       static_cast<const u32x4*>(b), static_cast<u32x4*>(y), n);
+  else
+    hipLaunchKernelGGL(stream_probe_kernel<false>, grid, dim3(kStreamThreads), 0, s, static_cast<const u32x4*>(a),
+                       nullptr, static_cast<u32x4*>(y), n);
+  return launched("pk_probe_stream");
+}
 
 int pk_probe_mfma(int softmax, int iters, int blocks, uint64_t* out, void* stream) {
   using namespace pk;

@@ -47,3 +47,29 @@ def test_probe_refuses_bad_arguments(lib):
     assert lib.pk_probe_mfma(0, 4, 0, out.data_ptr(), stream) == _lib.ERR_INVALID
     assert lib.pk_probe_mfma(0, 4, 1, None, stream) == _lib.ERR_INVALID
     assert "null pointer" in lib.pk_last_error().decode()
+
+
+@pytest.mark.parametrize("reads", [1, 2])
+def test_stream_probe_copies_or_combines(lib, reads):
+    nbytes = (3 << 20) + 48  # not a whole number of blocks: the last block is partial
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    a = torch.empty(nbytes, dtype=torch.uint8, device=DEV).random_(generator=gen)
+    b = torch.empty(nbytes, dtype=torch.uint8, device=DEV).random_(generator=gen)
+    y = torch.full((nbytes + 16,), 0x5A, dtype=torch.uint8, device=DEV)  # one guard vector past the end
+    print(f"[probe] stream reads={reads} bytes={nbytes}", flush=True)
+    _lib.check(lib.pk_probe_stream(a.data_ptr(), b.data_ptr() if reads == 2 else None, y.data_ptr(), nbytes, reads,
+                                   _lib.stream_handle(torch.device(DEV))), lib)
+    torch.cuda.synchronize()
+    want = a if reads == 1 else torch.bitwise_xor(a, b)
+    assert torch.equal(y[:nbytes], want)
+    assert bool((y[nbytes:] == 0x5A).all()), "the probe wrote past the end"
+
+
+def test_stream_probe_refuses_bad_arguments(lib):
+    a = torch.zeros(64, dtype=torch.uint8, device=DEV)
+    stream = _lib.stream_handle(torch.device(DEV))
+    assert lib.pk_probe_stream(a.data_ptr(), None, a.data_ptr(), 40, 1, stream) == _lib.ERR_INVALID  # not 16-byte units
+    assert lib.pk_probe_stream(a.data_ptr(), None, a.data_ptr(), 32, 3, stream) == _lib.ERR_INVALID
+    assert lib.pk_probe_stream(a.data_ptr(), None, a.data_ptr(), 32, 2, stream) == _lib.ERR_INVALID  # b missing
+    assert lib.pk_probe_stream(a.data_ptr() + 8, None, a.data_ptr(), 32, 1, stream) == _lib.ERR_INVALID
+    assert lib.pk_probe_stream(a.data_ptr(), None, a.data_ptr(), 0, 1, stream) == _lib.OK
