@@ -1,14 +1,19 @@
 """Benchmark of the MI355X transformer-block kernels on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-others]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--head-dim D] [--power]
+                    [--no-cpu] [--no-others]
 
 A step is one pass of a workload's drop-in call (the `popcorn_amd.impls`
 function Popcorn dispatches to) over one batch of synthetic input already
 resident in HBM. The default workload is BASELINE config 2 (SwiGLU forward,
 bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, `add_rmsnorm`
-(residual add + RMSNorm at C4's shape), `attn_bwd` (attention forward +
-backward at C5's shape), or `copy`, a plain device copy of known size used to
-calibrate HBM byte counters.
+(residual add + RMSNorm at C4's shape), `rope` and `qk_norm_rope` (forward +
+backward), `attn_bwd` (attention forward + backward at C5's shape), `c5_f32`
+(C5 in fp32), the ceilings `mfma_ceiling`, `mfma_ceiling_softmax` (matrix-core
+rate under the power limit) and `stream_<reads>r_<MiB>m` (streaming rate at a
+pattern and size), or `copy`, a plain device copy of known size used to
+calibrate HBM byte counters. `--head-dim` sets the attention workloads' head_dim;
+`--power` adds an `amd-smi` sample of socket power and clocks during a 6 s run.
 
 Rank 0 prints ONE JSON line. `value` is the workload's achieved algorithmic
 throughput (TB/s of HBM bytes for c1-c4, TFLOP/s for c5). `roofline` is the
@@ -38,6 +43,7 @@ import torch
 
 HBM_PEAK_TBS = 8.0  # MI355X HBM3E, TB/s
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA, TFLOP/s
 METRIC = "achieved HBM TB/s (norm/rope/swiglu) + attn-fwd bf16 TFLOP/s, % of peak"
 # A workload small enough to sit in the 256 MiB MALL (Infinity Cache) rotates through copies of its
 # inputs until the inputs alone span this many bytes, twice the MALL, so each launch reads from HBM.
@@ -82,6 +88,7 @@ class Workload:
     launch_kernels: tuple[str, ...] = ()
     # figures the workload reports beside its rate, read after the timed calls
     extra: Callable[[], dict] | None = None
+    peak: float | None = None  # the dominant kernel's peak in `unit` when it is not bf16 MFMA or HBM
 
 
 def _copies(nbytes: int) -> int:
@@ -467,11 +474,14 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
                          "dtype": "bf16"}, cpu, torch_step,
                         launch_kernels=("attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"))
 
-    if name == "c5":
+    if name in ("c5", "c5_f32"):
+        # c5_f32 (not a BASELINE config): C5's shape in fp32, on the fp32 matrix-core kernel
+        fp32 = name == "c5_f32"
+        dt, code = (torch.float32, _lib.F32) if fp32 else (torch.bfloat16, _lib.BF16)
         B, S, HQ, HKV, D = 4, 8192, 32, 8, head_dim
-        q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
-        k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
-        v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
+        q = _randn((B, S, HQ, D), dt, gen, dev)
+        k = _randn((B, S, HKV, D), dt, gen, dev)
+        v = _randn((B, S, HKV, D), dt, gen, dev)
         flops = 4.0 * B * HQ * D * S * S / 2
         o = torch.empty_like(q)
         lse = torch.empty((B, HQ, S), dtype=torch.float32, device=dev)
@@ -483,15 +493,15 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
 
         def launch(i):
             _lib.check(lib.pk_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
+                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, code, stream()))
 
         def cpu():
             # The largest of (B, S) = (1, 2048), (1, 4096), (1, 8192), (4, 8192) -- the last is C5
             # itself -- whose warmup plus two timed reps fit about 30 s on this host, estimated
             # from (1, 2048).
             def sample(b_cpu, s_cpu):
-                qc = torch.randn(b_cpu, s_cpu, HQ, D).bfloat16()
-                kc, vc = (torch.randn(b_cpu, s_cpu, HKV, D).bfloat16() for _ in range(2))
+                qc = torch.randn(b_cpu, s_cpu, HQ, D).to(dt)
+                kc, vc = (torch.randn(b_cpu, s_cpu, HKV, D).to(dt) for _ in range(2))
                 return lambda: R.attn(qc, kc, vc, True)
 
             probe = sample(1, 2048)
@@ -505,17 +515,18 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
             t, reps = _time_cpu(sample(b_cpu, s_cpu), budget_s=0.0, min_reps=2, max_reps=2)
             work = 4.0 * b_cpu * HQ * D * s_cpu * s_cpu / 2
             what = "full C5" if (b_cpu, s_cpu) == (B, S) else f"B={b_cpu}, S={s_cpu} of C5's B=4, S=8192"
-            return work / t / 1e12, f"{what}, causal bf16, 1 warmup + median of {reps} reps"
+            return work / t / 1e12, f"{what}, causal {'fp32' if fp32 else 'bf16'}, 1 warmup + median of {reps} reps"
 
         def torch_step(i):
             with torch.no_grad():
                 R.attn(q, k, v, True)
 
-        return Workload("c5" if D == 128 else f"c5_d{D}", f"Causal GQA attention fwd bf16 B=4 S=8192 Hq=32 Hkv=8 D={D}",
-                        "bf16", "TFLOP/s",
-                        flops, step, "attn_fwd_kernel", flops, launch,
+        tag = "fp32" if fp32 else "bf16"
+        return Workload(name if D == 128 else f"{name}_d{D}", f"Causal GQA attention fwd {tag} B=4 S=8192 Hq=32 Hkv=8 D={D}",
+                        "f32" if fp32 else "bf16", "TFLOP/s",
+                        flops, step, "attn_fwd_f32_kernel" if fp32 else "attn_fwd_kernel", flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
-                         "dtype": "bf16"}, cpu, torch_step)
+                         "dtype": tag}, cpu, torch_step, peak=FP32_PEAK_TFLOPS if fp32 else None)
 
     if name in ("mfma_ceiling", "mfma_ceiling_softmax"):
         # not a BASELINE config: the matrix-core rate this board sustains under its power limit,
@@ -674,7 +685,7 @@ def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
     avg = _time_gpu(wl.launch, steps, warmup) / steps
     achieved = _rate(wl.kernel_work, avg, wl.unit)
     hbm = wl.unit == "TB/s"
-    peak = HBM_PEAK_TBS if hbm else BF16_PEAK_TFLOPS
+    peak = wl.peak if wl.peak is not None else (HBM_PEAK_TBS if hbm else BF16_PEAK_TFLOPS)
     return {
         "kernel": wl.kernel,
         "bound": "hbm" if hbm else "mfma",
@@ -727,8 +738,8 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    named = ["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope", "attn_bwd", "mfma_ceiling",
-             "mfma_ceiling_softmax", "copy"]
+    named = ["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope", "attn_bwd", "c5_f32",
+             "mfma_ceiling", "mfma_ceiling_softmax", "copy"]
 
     def workload_name(text: str) -> str:
         if text in named or text.startswith("stream_"):

@@ -227,8 +227,10 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
  * o like q; q head h reads kv head h / (q_heads / kv_heads). causal = 1 masks
  * key j > query i (top-left aligned). lse (fp32 [batch, q_heads, seq],
  * natural log) may be NULL. strides[12] = q, k, v, o (batch, seq, head)
- * strides in elements. dtype is PK_BF16 or PK_F16; head_dim a multiple of 8
- * up to 256 (rows laid out at 64, 128 or 256 dims, zeros past head_dim).
+ * strides in elements. dtype is PK_BF16 or PK_F16 with head_dim a multiple of
+ * 8 up to 256 (rows laid out at 64, 128 or 256 dims, zeros past head_dim), or
+ * PK_F32 with head_dim a multiple of 8 up to 128 (the fp32 matrix-core kernel,
+ * exact online softmax; strides multiples of 4 elements).
  * Replaces: reference `attn` (kernels/attn.py:10-37,
  * F.scaled_dot_product_attention with enable_gqa=True).
  */

@@ -136,21 +136,21 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
     )
 
 
-def _attn_head_dim(head_dim: int, *tensors: Any) -> bool:
-    """Rows of whole 16-byte chunks: head_dim a multiple of 8 up to 256 for the forward kernel, up to 128
-    when autograd must record the call (the backward kernels' widest rows)."""
-    if head_dim % 8 or not 8 <= head_dim <= 256:
+def _attn_head_dim(head_dim: int, dtype: torch.dtype, *tensors: Any) -> bool:
+    """head_dim a multiple of 8: up to 256 for the 16-bit forward kernels and 128 for the fp32 one; when
+    autograd must record the call, 16-bit only and up to 128 (the backward kernels' widest rows)."""
+    if head_dim % 8 or not 8 <= head_dim <= (256 if dtype in _HALF else 128):
         return False
     records = torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
-    return head_dim <= 128 or not records
+    return not records or (dtype in _HALF and head_dim <= 128)
 
 
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:
     return (
         _on_hip(q, k, v)
-        and q.dtype in (torch.bfloat16, torch.float16)
+        and q.dtype in _FLOATS
         and q.dtype == k.dtype == v.dtype
-        and _attn_head_dim(q.shape[-1], q, k, v)
+        and _attn_head_dim(q.shape[-1], q.dtype, q, k, v)
         and k.shape[2] > 0
         and q.shape[2] % k.shape[2] == 0
     )
@@ -162,10 +162,10 @@ def attn_varlen_supported(q, k, v, cu_seqlens, causal, softmax_scale) -> bool:
         and isinstance(cu_seqlens, torch.Tensor)
         and not cu_seqlens.is_floating_point()
         and cu_seqlens.dim() == 1
-        and q.dtype in (torch.bfloat16, torch.float16)
+        and q.dtype in _FLOATS
         and q.dtype == k.dtype == v.dtype
         and q.dim() == 3
-        and _attn_head_dim(q.shape[-1], q, k, v)
+        and _attn_head_dim(q.shape[-1], q.dtype, q, k, v)
         and k.shape[1] > 0
         and q.shape[1] % k.shape[1] == 0
     )

@@ -457,6 +457,8 @@ namespace {
 // Checks shared by the dense and the packed entry point, then the launch.
 // strides: q, k, v, o (batch, token, head) in elements; `seq` is the longest
 // sequence, `batch` the number of sequences.
+#include "attn_fwd_f32.h"
+
 int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t batch, int64_t seq, int64_t q_heads,
                 int64_t kv_heads, int64_t head_dim, float softmax_scale, int causal, int dtype, void* stream) {
   if (batch < 0 || seq < 0 || q_heads < 0 || kv_heads < 0 || head_dim < 0)
@@ -466,17 +468,21 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   if (kv_heads == 0 || q_heads % kv_heads != 0)
     return fail(PK_ERR_INVALID, "%s: q_heads=%lld is not a multiple of kv_heads=%lld", who, (long long)q_heads,
                 (long long)kv_heads);
-  if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
-  if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
-    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to 256)", who, (long long)head_dim);
+  if (dtype != PK_BF16 && dtype != PK_F16 && dtype != PK_F32)
+    return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16/fp32 only)", who, dtype);
+  const int max_dim = dtype == PK_F32 ? 128 : 256;
+  if (head_dim <= 0 || head_dim > max_dim || head_dim % 8 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to %d for this dtype)", who,
+                (long long)head_dim, max_dim);
   if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
   if (seq > (1 << 30) || batch * q_heads > (1 << 20)) return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
   if (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.o))
     return fail(PK_ERR_INVALID, "%s: q/k/v/o must be 16-byte aligned", who);
+  const int unit = dtype == PK_F32 ? 4 : 8;  // elements per 16 bytes
   for (int i = 0; i < 12; ++i)
-    if (strides[i] % 8 != 0 || strides[i] < 0)
-      return fail(PK_ERR_INVALID, "%s: stride %d = %lld is not a non-negative multiple of 8", who, i,
-                  (long long)strides[i]);
+    if (strides[i] % unit != 0 || strides[i] < 0)
+      return fail(PK_ERR_INVALID, "%s: stride %d = %lld is not a non-negative multiple of %d", who, i,
+                  (long long)strides[i], unit);
   a.qsb = strides[0];
   a.qss = strides[1];
   a.qsh = strides[2];
@@ -499,15 +505,18 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   // Buffer offsets are 32-bit: within one sequence the tile loads reach up to
   // two tiles past its last row (reading zeros there), and every such offset
   // must fit.
+  // (the fp32 kernel addresses with 64-bit pointers)
   const int64_t reach = (seq + 3 * BN) * (strides[4] > strides[7] ? strides[4] : strides[7]) * 2 + head_dim * 2;
-  if (reach > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: K/V rows span more than 2 GiB per head", who);
+  if (dtype != PK_F32 && reach > INT32_MAX)
+    return fail(PK_ERR_UNSUPPORTED, "%s: K/V rows span more than 2 GiB per head", who);
   a.c = fmaxf(fabsf(softmax_scale) * 1.4426950408889634f, 1e-30f);
   a.q_flip = softmax_scale < 0.f ? 0x80008000u : 0u;
   a.dr = (int)head_dim;
   a.dch = (int)(head_dim / 8);
   if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
+  // rows are laid out at 64, 128 or 256 dims, the chunks past head_dim reading as zeros
+  if (dtype == PK_F32) return head_dim <= 64 ? launch_f32<64>(a, causal, s) : launch_f32<128>(a, causal, s);
   if (dtype == PK_BF16)
     return head_dim <= 64 ? launch<bf16, 64>(a, causal, s)
                           : head_dim <= 128 ? launch<bf16, 128>(a, causal, s) : launch<bf16, 256>(a, causal, s);

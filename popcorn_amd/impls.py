@@ -620,17 +620,20 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
     """softmax(q k^T * scale + causal mask) v with grouped kv heads.
 
     q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim];
-    bf16 or fp16; head_dim a multiple of 8 up to 256 (up to 128 with
-    gradients); scale defaults to head_dim ** -0.5. Backward gives dq, dk, dv.
+    bf16 or fp16 with head_dim a multiple of 8 up to 256 (up to 128 with
+    gradients), or fp32 up to 128 (forward only); scale defaults to
+    head_dim ** -0.5. Backward gives dq, dk, dv.
     """
     if _tracks_grad(q, k, v):
-        _grad_head_dim("attn", q.shape[-1])
+        _grad_supported("attn", q.shape[-1], q.dtype)
         return _Attention.apply(q, k, v, causal, softmax_scale)
     return _attn_fwd(q, k, v, causal, softmax_scale, want_lse=False)[0]
 
 
-def _grad_head_dim(op: str, head_dim: int) -> None:
+def _grad_supported(op: str, head_dim: int, dtype: torch.dtype) -> None:
     """Refuse, before any work, a call whose backward the kernels do not cover."""
+    if dtype not in _HALF:
+        raise ValueError(f"popcorn_amd.{op}: {dtype} has a forward kernel only (gradients in bf16 and fp16)")
     if head_dim > 128:
         raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} has a forward kernel only (gradients up to 128)")
 
@@ -702,7 +705,8 @@ class _Attention(torch.autograd.Function):
 
 def _aligned_rows(t: Tensor) -> Tensor:
     """A view the kernel can read with 16-byte loads, copying only when it must."""
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % 8 == 0 and s >= 0 for s in t.stride()[:-1])
+    unit = 16 // t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all(s % unit == 0 and s >= 0 for s in t.stride()[:-1])
     if ok:
         return t
     c = t.contiguous()
@@ -729,7 +733,7 @@ def attn_varlen(
     """
     cu, num_seqs, longest = _cut_points(cu_seqlens, q.shape[0], q.device)
     if _tracks_grad(q, k, v):
-        _grad_head_dim("attn_varlen", q.shape[-1])
+        _grad_supported("attn_varlen", q.shape[-1], q.dtype)
         return _AttentionVarlen.apply(q, k, v, cu, num_seqs, longest, causal, softmax_scale)
     return _attn_varlen_fwd(q, k, v, cu, num_seqs, longest, causal, softmax_scale, want_lse=False)[0]
 

@@ -40,6 +40,8 @@ def gauge_ok(mine, truth, ref_native, dtype: torch.dtype, what: str = "out") -> 
     t = _as64(truth)
     err = max_err(mine, t)
     budget = max_err(ref_native, t)
+    # a reference that is not finite where the truth is would make any error pass
+    assert math.isfinite(budget), f"{what}: the native-dtype reference is not finite against the float64 truth"
     scale = max(1.0, float(np.abs(t).max()) if t.size else 1.0)
     limit = max(2 * budget, floor * scale)
     assert math.isfinite(err) and err <= limit, (

@@ -100,14 +100,44 @@ def test_attention_predicates_cover_the_head_dims(monkeypatch):
     assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), True, None)
 
 
+def test_attention_predicates_take_fp32_forward_only(monkeypatch):
+    """fp32 attention runs the fp32 forward kernel, head_dim up to 128; with gradients to record it is
+    declined (no fp32 backward kernel), so Popcorn serves it with torch."""
+    monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
+
+    def qkv(d, grad=False):
+        q = torch.empty(1, 16, 8, d, dtype=torch.float32, device="meta")
+        k = torch.empty(1, 16, 2, d, dtype=torch.float32, device="meta")
+        return [t.requires_grad_(grad) for t in (q, k, k.clone())]
+
+    for d in (16, 32, 64, 96, 128):
+        assert backend.attn_supported(*qkv(d), True, None)
+        assert not backend.attn_supported(*qkv(d, grad=True), True, None)
+        with torch.no_grad():
+            assert backend.attn_supported(*qkv(d, grad=True), True, None)
+        q, k, v = (t[0] for t in qkv(d))
+        assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), False, None)
+    for d in (192, 256, 100):
+        assert not backend.attn_supported(*qkv(d), True, None)
+
+
 def test_attention_with_gradients_past_head_dim_128_is_refused_before_any_work():
     from popcorn_amd import impls
 
-    q = torch.randn(1, 4, 2, 192, requires_grad=True)  # CPU tensors: the refusal comes first
+    q = torch.randn(1, 4, 2, 192).bfloat16().requires_grad_()  # CPU tensors: the refusal comes first
     for call in (lambda: impls.attn(q, q, q, True), lambda: impls.attn_varlen(q[0], q[0], q[0], torch.tensor([0, 4]))):
         try:
             call()
         except ValueError as e:
-            assert "forward kernel only" in str(e)
+            assert "head_dim=192 has a forward kernel only" in str(e)
         else:
             raise AssertionError("head_dim 192 with gradients was not refused")
+    q32 = torch.randn(1, 4, 2, 64, requires_grad=True)  # fp32: no backward kernel at any head_dim
+    for call in (lambda: impls.attn(q32, q32, q32, True),
+                 lambda: impls.attn_varlen(q32[0], q32[0], q32[0], torch.tensor([0, 4]))):
+        try:
+            call()
+        except ValueError as e:
+            assert "torch.float32 has a forward kernel only" in str(e)
+        else:
+            raise AssertionError("fp32 attention with gradients was not refused")

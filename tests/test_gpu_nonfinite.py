@@ -107,16 +107,18 @@ def test_rope_nonfinite():
     _same_pattern(mk, rk, "rope k")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-def test_attn_nonfinite_key_and_value(causal):
+def test_attn_nonfinite_key_and_value(causal, dtype):
     """A NaN in key 5 of kv head 0 makes every query of that group that sees key 5 NaN (all of them
     without the mask, rows 5 on with it); an Inf in a value row makes those queries' outputs in that
-    dim Inf or NaN exactly as the reference's softmax-weighted sum does; other heads stay finite."""
+    dim Inf or NaN exactly as the reference's softmax-weighted sum does; other heads stay finite.
+    fp32 runs the fp32 kernel's online softmax, bf16 the fixed-max sweep and its exact resweep."""
     b, s, hq, hkv, d = 1, 64, 4, 2, 64
-    q = seeded((b, s, hq, d), 13, torch.bfloat16)
-    k = _plant(seeded((b, s, hkv, d), 14, torch.bfloat16), [((0, 5, 0, 3), NAN)])
-    v = _plant(seeded((b, s, hkv, d), 15, torch.bfloat16), [((0, 40, 1, 7), INF)])
+    q = seeded((b, s, hq, d), 13, dtype)
+    k = _plant(seeded((b, s, hkv, d), 14, dtype), [((0, 5, 0, 3), NAN)])
+    v = _plant(seeded((b, s, hkv, d), 15, dtype), [((0, 40, 1, 7), INF)])
     with torch.no_grad():
         ref = R.attn(q, k, v, causal)
         mine = impls.attn(q.to(DEV), k.to(DEV), v.to(DEV), causal)
-    _same_pattern(mine, ref, f"attn causal={causal}")
+    _same_pattern(mine, ref, f"attn {dtype} causal={causal}")
