@@ -9,8 +9,9 @@ resident in HBM. The default workload is BASELINE config 2 (SwiGLU forward,
 bf16, a, b [16384, 14336]); `--workload` picks any of c1..c5, `add_rmsnorm`
 (residual add + RMSNorm at C4's shape), `rope` and `qk_norm_rope` (forward +
 backward), `attn_bwd` (attention forward + backward at C5's shape), `c5_f32`
-(C5 in fp32), the ceilings `mfma_ceiling`, `mfma_ceiling_softmax` (matrix-core
-rate under the power limit) and `stream_<reads>r_<MiB>m` (streaming rate at a
+and `attn_bwd_f32` (the same two in fp32), the ceilings `mfma_ceiling`,
+`mfma_ceiling_softmax` (matrix-core rate under the power limit) and
+`stream_<reads>r_<MiB>m` (streaming rate at a
 pattern and size), or `copy`, a plain device copy of known size used to
 calibrate HBM byte counters. `--head-dim` sets the attention workloads' head_dim;
 `--power` adds an `amd-smi` sample of socket power and clocks during a 6 s run.
@@ -424,13 +425,16 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
                         {"rows": rows, "cols": cols, "eps": 1e-6, "offset": 1.0, "dtype": "bf16"}, cpu, torch_step,
                         launch_kernels=("rmsnorm_bwd_vec", "column_sum_stage", "column_sum_final"))
 
-    if name == "attn_bwd":
-        # not a BASELINE config: attention forward + backward at C5's shape (bf16, causal)
+    if name in ("attn_bwd", "attn_bwd_f32"):
+        # not a BASELINE config: attention forward + backward at C5's shape (causal), bf16 or, for
+        # attn_bwd_f32, fp32 on the fp32 matrix-core kernels
+        fp32 = name == "attn_bwd_f32"
+        dt, code, tag = (torch.float32, _lib.F32, "fp32") if fp32 else (torch.bfloat16, _lib.BF16, "bf16")
         B, S, HQ, HKV, D = 4, 8192, 32, 8, head_dim
-        q = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
-        k = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
-        v = _randn((B, S, HKV, D), torch.bfloat16, gen, dev)
-        do = _randn((B, S, HQ, D), torch.bfloat16, gen, dev)
+        q = _randn((B, S, HQ, D), dt, gen, dev)
+        k = _randn((B, S, HKV, D), dt, gen, dev)
+        v = _randn((B, S, HKV, D), dt, gen, dev)
+        do = _randn((B, S, HQ, D), dt, gen, dev)
         fwd_flops = 4.0 * B * HQ * D * S * S / 2
         bwd_flops = 2.5 * fwd_flops  # the customary count: dQ, dK, dV, dP and S recomputed once (5 products)
         qg, kg, vg = (t.detach().requires_grad_() for t in (q, k, v))
@@ -447,13 +451,13 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
             _lib.check(lib.pk_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
                                        lse.data_ptr(), ws.data_ptr(), ws.numel(), dq.data_ptr(), dk.data_ptr(),
                                        dv.data_ptr(),
-                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, _lib.BF16, stream()))
+                                       strides, B, S, HQ, HKV, D, D**-0.5, 1, code, stream()))
 
         def cpu():
             sq = 1024  # one (batch, kv group) of 1024 tokens; work scaled to that
-            qc = torch.randn(1, sq, 4, D).bfloat16().requires_grad_()
-            kc, vc = (torch.randn(1, sq, 1, D).bfloat16().requires_grad_() for _ in range(2))
-            gc = torch.randn(1, sq, 4, D).bfloat16()
+            qc = torch.randn(1, sq, 4, D).to(dt).requires_grad_()
+            kc, vc = (torch.randn(1, sq, 1, D).to(dt).requires_grad_() for _ in range(2))
+            gc = torch.randn(1, sq, 4, D).to(dt)
 
             def one():
                 oc = R.attn(qc, kc, vc, True)
@@ -461,18 +465,20 @@ def make_workload(name: str, dev: torch.device, head_dim: int = 128) -> Workload
 
             t, reps = _time_cpu(one)
             work = 3.5 * 4.0 * 4 * D * sq * sq / 2
-            return work / t / 1e12, f"B=1, S={sq}, Hq=4, Hkv=1 causal fwd+bwd bf16, median of {reps} reps"
+            return work / t / 1e12, f"B=1, S={sq}, Hq=4, Hkv=1 causal fwd+bwd {tag}, median of {reps} reps"
 
         def torch_step(i):
             out = R.attn(qg, kg, vg, True)
             torch.autograd.grad(out, (qg, kg, vg), do)
 
-        return Workload("attn_bwd" if D == 128 else f"attn_bwd_d{D}",
-                        f"Causal GQA attention fwd+bwd bf16 B=4 S=8192 Hq=32 Hkv=8 D={D}", "bf16",
+        kernels = ("attn_bwd_f32_dq_kernel", "attn_bwd_f32_dkdv_kernel") if fp32 else \
+            ("attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel")
+        return Workload(name if D == 128 else f"{name}_d{D}",
+                        f"Causal GQA attention fwd+bwd {tag} B=4 S=8192 Hq=32 Hkv=8 D={D}", "f32" if fp32 else "bf16",
                         "TFLOP/s", fwd_flops + bwd_flops, step, "attn_bwd", bwd_flops, launch,
                         {"batch": B, "seq": S, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "causal": True,
-                         "dtype": "bf16"}, cpu, torch_step,
-                        launch_kernels=("attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"))
+                         "dtype": tag}, cpu, torch_step, launch_kernels=kernels,
+                        peak=FP32_PEAK_TFLOPS if fp32 else None)
 
     if name in ("c5", "c5_f32"):
         # c5_f32 (not a BASELINE config): C5's shape in fp32, on the fp32 matrix-core kernel
@@ -738,7 +744,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    named = ["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope", "attn_bwd", "c5_f32",
+    named = ["c1", "c2", "c3", "c4", "c5", "add_rmsnorm", "rope", "qk_norm_rope", "attn_bwd", "c5_f32", "attn_bwd_f32",
              "mfma_ceiling", "mfma_ceiling_softmax", "copy"]
 
     def workload_name(text: str) -> str:

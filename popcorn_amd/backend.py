@@ -138,11 +138,11 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
 
 def _attn_head_dim(head_dim: int, dtype: torch.dtype, *tensors: Any) -> bool:
     """head_dim a multiple of 8: up to 256 for the 16-bit forward kernels and 128 for the fp32 one; when
-    autograd must record the call, 16-bit only and up to 128 (the backward kernels' widest rows)."""
+    autograd must record the call, up to 128 (the backward kernels' widest rows, in every dtype)."""
     if head_dim % 8 or not 8 <= head_dim <= (256 if dtype in _HALF else 128):
         return False
     records = torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
-    return not records or (dtype in _HALF and head_dim <= 128)
+    return not records or head_dim <= 128
 
 
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:

@@ -753,9 +753,14 @@ __global__ __launch_bounds__(256) void dkdv_sum_kernel(BwdArgs a) {
     }
     T* out = role == 0 ? static_cast<T*>(a.dv) + b * a.dvs[0] + t * a.dvs[1] + hkv * a.dvs[2]
                        : static_cast<T*>(a.dk) + b * a.dks[0] + t * a.dks[1] + hkv * a.dks[2];
-    *reinterpret_cast<uint2*>(out + d4) = pack4<T>(s.x, s.y, s.z, s.w);
+    if constexpr (std::is_same<T, float>::value)
+      *reinterpret_cast<float4*>(out + d4) = s;
+    else
+      *reinterpret_cast<uint2*>(out + d4) = pack4<T>(s.x, s.y, s.z, s.w);
   }
 }
+
+#include "attn_bwd_f32.h"
 
 template <typename T, int D>
 int launch(const BwdArgs& a, bool causal, hipStream_t s) {
@@ -819,7 +824,8 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   if (!aligned16(workspace)) return fail(PK_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
   a.dsum = static_cast<float*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(2 * a.lse_n * (int64_t)sizeof(float)));
-  if (dtype != PK_BF16 && dtype != PK_F16) return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16 only)", who, dtype);
+  if (dtype != PK_BF16 && dtype != PK_F16 && dtype != PK_F32)
+    return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16/fp32 only)", who, dtype);
   if (head_dim <= 0 || head_dim > 128 || head_dim % 8 != 0)
     return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to 128)", who, (long long)head_dim);
   if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
@@ -827,17 +833,19 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   const void* ptrs[] = {a.q, a.k, a.v, a.o, a.dout, a.dq, a.dk, a.dv};
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(PK_ERR_INVALID, "%s: tensors must be 16-byte aligned", who);
+  const int64_t elem = dtype == PK_F32 ? 4 : 2;
+  const int64_t unit = 16 / elem;  // strides in whole 16-byte chunks
   for (int i = 0; i < 24; ++i)
-    if (strides[i] % 8 != 0 || strides[i] < 0)
-      return fail(PK_ERR_INVALID, "%s: stride %d = %lld is not a non-negative multiple of 8", who, i,
-                  (long long)strides[i]);
+    if (strides[i] % unit != 0 || strides[i] < 0)
+      return fail(PK_ERR_INVALID, "%s: stride %d = %lld is not a non-negative multiple of %lld", who, i,
+                  (long long)strides[i], (long long)unit);
   int64_t* dst[] = {a.qs, a.ks, a.vs, a.os, a.gs, a.dqs, a.dks, a.dvs};
   for (int t = 0; t < 8; ++t)
     for (int i = 0; i < 3; ++i) dst[t][i] = strides[3 * t + i];
   // buffer offsets are 32-bit: rows of one sequence (plus a tile past the end) must fit
   int64_t widest = 0;
   for (int t = 0; t < 5; ++t) widest = dst[t][1] > widest ? dst[t][1] : widest;
-  if ((seq + 2 * BK) * widest * 2 + head_dim * 2 > INT32_MAX)
+  if ((seq + 2 * BK) * widest * elem + head_dim * elem > INT32_MAX)
     return fail(PK_ERR_UNSUPPORTED, "%s: rows span more than 2 GiB per head", who);
   a.B = (int)batch;
   a.S = (int)seq;
@@ -852,6 +860,7 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
+  if (dtype == PK_F32) return head_dim <= 64 ? launch_f32<64>(a, causal, s) : launch_f32<128>(a, causal, s);
   if (dtype == PK_BF16) return head_dim <= 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
   return head_dim <= 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
 }

@@ -631,9 +631,7 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
 
 
 def _grad_supported(op: str, head_dim: int, dtype: torch.dtype) -> None:
-    """Refuse, before any work, a call whose backward the kernels do not cover."""
-    if dtype not in _HALF:
-        raise ValueError(f"popcorn_amd.{op}: {dtype} has a forward kernel only (gradients in bf16 and fp16)")
+    """Refuse, before any work, a call whose backward the kernels do not cover (head_dim above 128)."""
     if head_dim > 128:
         raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} has a forward kernel only (gradients up to 128)")
 

@@ -100,9 +100,8 @@ def test_attention_predicates_cover_the_head_dims(monkeypatch):
     assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), True, None)
 
 
-def test_attention_predicates_take_fp32_forward_only(monkeypatch):
-    """fp32 attention runs the fp32 forward kernel, head_dim up to 128; with gradients to record it is
-    declined (no fp32 backward kernel), so Popcorn serves it with torch."""
+def test_attention_predicates_take_fp32(monkeypatch):
+    """fp32 attention runs the fp32 kernels, head_dim up to 128, with or without gradients to record."""
     monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
 
     def qkv(d, grad=False):
@@ -112,13 +111,12 @@ def test_attention_predicates_take_fp32_forward_only(monkeypatch):
 
     for d in (16, 32, 64, 96, 128):
         assert backend.attn_supported(*qkv(d), True, None)
-        assert not backend.attn_supported(*qkv(d, grad=True), True, None)
-        with torch.no_grad():
-            assert backend.attn_supported(*qkv(d, grad=True), True, None)
-        q, k, v = (t[0] for t in qkv(d))
+        assert backend.attn_supported(*qkv(d, grad=True), True, None)
+        q, k, v = (t[0] for t in qkv(d, grad=True))
         assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), False, None)
     for d in (192, 256, 100):
         assert not backend.attn_supported(*qkv(d), True, None)
+        assert not backend.attn_supported(*qkv(d, grad=True), True, None)
 
 
 def test_attention_with_gradients_past_head_dim_128_is_refused_before_any_work():
@@ -132,12 +130,12 @@ def test_attention_with_gradients_past_head_dim_128_is_refused_before_any_work()
             assert "head_dim=192 has a forward kernel only" in str(e)
         else:
             raise AssertionError("head_dim 192 with gradients was not refused")
-    q32 = torch.randn(1, 4, 2, 64, requires_grad=True)  # fp32: no backward kernel at any head_dim
+    q32 = torch.randn(1, 4, 2, 192, requires_grad=True)
     for call in (lambda: impls.attn(q32, q32, q32, True),
                  lambda: impls.attn_varlen(q32[0], q32[0], q32[0], torch.tensor([0, 4]))):
         try:
             call()
         except ValueError as e:
-            assert "torch.float32 has a forward kernel only" in str(e)
+            assert "head_dim=192" in str(e)
         else:
-            raise AssertionError("fp32 attention with gradients was not refused")
+            raise AssertionError("fp32 head_dim 192 with gradients was not refused")
