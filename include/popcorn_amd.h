@@ -276,8 +276,8 @@ int64_t pk_attn_bwd_workspace(int64_t batch, int64_t seq, int64_t q_heads, int64
  * (partials of q-head splits are added in a fixed order, so the result is
  * deterministic). strides[24] = q, k, v, o, dout, dq, dk, dv (batch, token,
  * head) strides in elements, multiples of 8 (bf16, fp16) or 4 (fp32).
- * head_dim a multiple of 8 up to 128. dtype PK_BF16, PK_F16 or PK_F32 (the
- * fp32 matrix-core kernels, v_mfma_f32_32x32x2_f32).
+ * head_dim a multiple of 8 up to 256 (bf16, fp16) or 128 (PK_F32, the fp32
+ * matrix-core kernels, v_mfma_f32_32x32x2_f32).
  * Replaces torch autograd of the reference `attn` (kernels/attn.py:30-37).
  */
 int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,

@@ -48,11 +48,15 @@
 // signed c and the signed scale for dK.
 //
 // LDS tiles are unpadded rows of 16-byte chunks, chunk c of row r stored at
-// c ^ swz(r): swz(r) = 4 (r % 4) + (r / 4) % 4 for head_dim 128 (rows span all
-// 64 banks) and 4 ((r / 2) % 2) + (r / 4) % 4 for head_dim 64 (two rows per
-// bank sweep). Either way the 16-byte fragment reads (16 rows, one chunk) and
-// the transposing ds_read_b64_tr_b16 reads (4 rows x 4 chunks per pair of
-// 16-lane groups) land on 64 distinct banks.
+// c ^ swz(r): swz(r) = 4 (r % 4) + (r / 4) % 4 for head_dim 128 and 256 (rows
+// span all 64 banks, or twice) and 4 ((r / 2) % 2) + (r / 4) % 4 for head_dim
+// 64 (two rows per bank sweep). Either way the 16-byte fragment reads (16
+// rows, one chunk) and the transposing ds_read_b64_tr_b16 reads (4 rows x 4
+// chunks per pair of 16-lane groups) land on 64 distinct banks.
+//
+// head_dim 256 (attn_bwd_wide.h) keeps this dq kernel, at one wave per SIMD,
+// and replaces the dkdv kernel, whose six stages would not fit in LDS at that
+// width, with a single-role kernel.
 #include <math.h>
 
 #include <type_traits>
@@ -105,10 +109,12 @@ struct BwdArgs {
 constexpr uint32_t kPadOffset = 0x80000000u;
 
 // LDS tile layout: unpadded rows, 16-byte chunk c of row r at c ^ swz(r)
+// (head_dim 256 rows span two bank sweeps; chunk c % 16 picks the banks, so
+// they take head_dim 128's swizzle)
 template <int D> struct Tile {
   static constexpr int ST = D;
   static __device__ __forceinline__ int swz(int row) {
-    if constexpr (D == 128)
+    if constexpr (D >= 128)
       return 4 * (row & 3) + ((row >> 2) & 3);
     else
       return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
@@ -132,13 +138,14 @@ __device__ __forceinline__ uint4 flip(uint4 v, uint32_t f) { return make_uint4(v
 
 // ------------------------------------------------------------------ dq kernel
 
+// head_dim 256 holds Q, dO and the dQ accumulator in 256 registers: one wave per SIMD
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_bwd_dq_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void attn_bwd_dq_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
   constexpr int KCH = D / 8;
-  constexpr int TI = BN * KCH / NT;  // direct loads per thread per tile of K (and of V): 2 or 1
+  constexpr int TI = BN * KCH / NT;  // direct loads per thread per tile of K (and of V): 4, 2 or 1
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   constexpr int NSQ = 4;  // K/V tile stages: the two tiles a step reads, one in flight, one landing
@@ -761,6 +768,7 @@ __global__ __launch_bounds__(256) void dkdv_sum_kernel(BwdArgs a) {
 }
 
 #include "attn_bwd_f32.h"
+#include "attn_bwd_wide.h"
 
 template <typename T, int D>
 int launch(const BwdArgs& a, bool causal, hipStream_t s) {
@@ -797,9 +805,9 @@ inline int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; 
 
 // Workspace bytes: D and lse2 (2 * lse_n floats), then the dk/dv partials when
 // the kernel splits the q heads.
-// (The partials are laid out at the kernels' row width: 64 or 128 dims.)
+// (The partials are laid out at the kernels' row width: 64, 128 or 256 dims.)
 int64_t workspace_bytes(int64_t lse_n, int64_t rows, int64_t kv_heads, int64_t head_dim, int nsplit) {
-  const int64_t width = head_dim <= 64 ? 64 : 128;
+  const int64_t width = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
   const int64_t parts = nsplit > 1 ? (int64_t)nsplit * 2 * rows * kv_heads * width * (int64_t)sizeof(float) : 0;
   return round_up(2 * lse_n * (int64_t)sizeof(float)) + parts;
 }
@@ -826,8 +834,10 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(2 * a.lse_n * (int64_t)sizeof(float)));
   if (dtype != PK_BF16 && dtype != PK_F16 && dtype != PK_F32)
     return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16/fp32 only)", who, dtype);
-  if (head_dim <= 0 || head_dim > 128 || head_dim % 8 != 0)
-    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to 128)", who, (long long)head_dim);
+  const int64_t max_dim = dtype == PK_F32 ? 128 : 256;
+  if (head_dim <= 0 || head_dim > max_dim || head_dim % 8 != 0)
+    return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to %lld)", who, (long long)head_dim,
+                (long long)max_dim);
   if (!isfinite(softmax_scale)) return fail(PK_ERR_INVALID, "%s: softmax_scale is not finite", who);
   if (seq > (1 << 30) || batch * q_heads > (1 << 20)) return fail(PK_ERR_UNSUPPORTED, "%s: shape too large", who);
   const void* ptrs[] = {a.q, a.k, a.v, a.o, a.dout, a.dq, a.dk, a.dv};
@@ -861,6 +871,7 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   hipStream_t s = static_cast<hipStream_t>(stream);
   // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
   if (dtype == PK_F32) return head_dim <= 64 ? launch_f32<64>(a, causal, s) : launch_f32<128>(a, causal, s);
+  if (head_dim > 128) return dtype == PK_BF16 ? launch_wide<bf16>(a, causal, s) : launch_wide<f16>(a, causal, s);
   if (dtype == PK_BF16) return head_dim <= 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
   return head_dim <= 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
 }

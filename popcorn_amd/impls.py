@@ -631,9 +631,11 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
 
 
 def _grad_supported(op: str, head_dim: int, dtype: torch.dtype) -> None:
-    """Refuse, before any work, a call whose backward the kernels do not cover (head_dim above 128)."""
-    if head_dim > 128:
-        raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} has a forward kernel only (gradients up to 128)")
+    """Refuse, before any work, a call whose backward the kernels do not cover: head_dim above 256 (16-bit)
+    or 128 (fp32), where the forward kernels stop too."""
+    widest = 256 if dtype in _HALF else 128
+    if head_dim > widest:
+        raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} is past the {dtype} kernels' {widest}")
 
 
 def _scale(head_dim: int, softmax_scale: float | None) -> float:

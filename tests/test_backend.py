@@ -80,8 +80,8 @@ def test_predicates_cover_the_mixed_dtype_pairs(monkeypatch):
 
 
 def test_attention_predicates_cover_the_head_dims(monkeypatch):
-    """Forward at every head_dim that is a multiple of 8 up to 256 (Popcorn's grid, core/dims.py:74);
-    with gradients to record up to 128, the backward kernels' widest rows; other widths declined."""
+    """Forward and backward at every head_dim that is a multiple of 8 up to 256 (Popcorn's grid,
+    core/dims.py:74); other widths declined."""
     monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
 
     def qkv(d, grad=False):
@@ -91,9 +91,7 @@ def test_attention_predicates_cover_the_head_dims(monkeypatch):
 
     for d in (16, 32, 48, 64, 80, 96, 128, 192, 256):
         assert backend.attn_supported(*qkv(d), True, None)
-        assert backend.attn_supported(*qkv(d, grad=True), True, None) == (d <= 128)
-        with torch.no_grad():  # nothing recorded: the forward kernel serves any of them
-            assert backend.attn_supported(*qkv(d, grad=True), True, None)
+        assert backend.attn_supported(*qkv(d, grad=True), True, None)
     for d in (8 * 33, 72 + 4, 100, 4):
         assert not backend.attn_supported(*qkv(d), True, None)
     q, k, v = (t[0] for t in qkv(96))
@@ -119,23 +117,17 @@ def test_attention_predicates_take_fp32(monkeypatch):
         assert not backend.attn_supported(*qkv(d, grad=True), True, None)
 
 
-def test_attention_with_gradients_past_head_dim_128_is_refused_before_any_work():
+def test_attention_with_gradients_past_the_kernels_is_refused_before_any_work():
     from popcorn_amd import impls
 
-    q = torch.randn(1, 4, 2, 192).bfloat16().requires_grad_()  # CPU tensors: the refusal comes first
-    for call in (lambda: impls.attn(q, q, q, True), lambda: impls.attn_varlen(q[0], q[0], q[0], torch.tensor([0, 4]))):
-        try:
-            call()
-        except ValueError as e:
-            assert "head_dim=192 has a forward kernel only" in str(e)
-        else:
-            raise AssertionError("head_dim 192 with gradients was not refused")
-    q32 = torch.randn(1, 4, 2, 192, requires_grad=True)
-    for call in (lambda: impls.attn(q32, q32, q32, True),
-                 lambda: impls.attn_varlen(q32[0], q32[0], q32[0], torch.tensor([0, 4]))):
-        try:
-            call()
-        except ValueError as e:
-            assert "head_dim=192" in str(e)
-        else:
-            raise AssertionError("fp32 head_dim 192 with gradients was not refused")
+    for q, what in ((torch.randn(1, 4, 2, 192, requires_grad=True), "head_dim=192 is past the torch.float32"),
+                    (torch.randn(1, 4, 2, 264).bfloat16().requires_grad_(), "head_dim=264 is past the torch.bfloat16")):
+        # CPU tensors: the refusal comes first
+        for call in (lambda: impls.attn(q, q, q, True),
+                     lambda: impls.attn_varlen(q[0], q[0], q[0], torch.tensor([0, 4]))):
+            try:
+                call()
+            except ValueError as e:
+                assert what in str(e), str(e)
+            else:
+                raise AssertionError(f"{what} with gradients was not refused")

@@ -253,3 +253,79 @@ def test_attn_varlen_bwd_dkdv_direct_and_partial_splits(seqs, length, splits):
         seg_grads = [g[rows].unsqueeze(0) for g in grads]
         _check_group_slices(*seg_view, seg_grads, True, dtype, [(0, 0), (0, hkv - 1)],
                             f"varlen {splits} split(s), sequence {seg}")
+
+
+# --------------------------------------------------------------------------- head_dim 136-256
+# Rows past 128 dims take the dq kernel at 256 and the single-role dk/dv kernel.
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("d", [256, 192])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("seq", [1, 17, 130, 257])
+def test_attn_bwd_wide_head_dims(seq, causal, d, dtype):
+    _check(2, seq, 8, 2, d, causal, None, dtype)
+
+
+@pytest.mark.parametrize("d", [136, 160, 248])
+def test_attn_bwd_wide_head_dims_laid_out_at_256(d):
+    """head_dim between 128 and 256: the dims past it read as zeros and are never stored."""
+    _check(1, 77, 4, 1, d, True, None, torch.bfloat16, seed=4)
+
+
+@pytest.mark.parametrize("heads", [(8, 8), (8, 1), (6, 2), (12, 2)], ids=str)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_attn_bwd_wide_groups(heads, causal):
+    _check(2, 150, heads[0], heads[1], 256, causal, None, torch.bfloat16, seed=11)
+
+
+@pytest.mark.parametrize("scale", [0.25, -0.3])
+def test_attn_bwd_wide_scales(scale):
+    _check(1, 96, 4, 2, 256, False, scale, torch.bfloat16, seed=9)
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("total,segments", [(300, 3), (129, 129)])
+def test_attn_varlen_bwd_wide(total, segments, causal):
+    _check_varlen(total, segments, 256, causal, torch.bfloat16)
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,d,dtype,causal,splits", [
+    (8, 1024, 32, 8, 256, torch.bfloat16, True, 1),    # 512 blocks: direct
+    (4, 1024, 32, 8, 256, torch.float16, False, 2),    # 256 blocks: two splits of two q heads
+    (2, 1024, 16, 2, 192, torch.bfloat16, True, 8),    # 32 blocks, group 8: one q head per block
+], ids=["direct-d256-bf16-causal", "split2-d256-fp16-full", "split8-d192-bf16-causal"])
+def test_attn_bwd_wide_dkdv_direct_and_partial_splits(b, s, hq, hkv, d, dtype, causal, splits):
+    lib = _lib.load()
+    assert _splits(lib.pk_attn_bwd_workspace(b, s, hq, hkv, d), b * hq * s, b * s, hkv, 256) == splits
+    print(f"[attn bwd wide] b={b} s={s} hq={hq} hkv={hkv} d={d} {dtype} causal={causal} splits={splits}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(17)
+    q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    k, v = (torch.randn(b, s, hkv, d, generator=gen, device=DEV).to(dtype) for _ in range(2))
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    grads = torch.autograd.grad(impls.attn(*leaves, causal), leaves, do)
+    _check_group_slices(q, k, v, do, grads, causal, dtype, [(0, 0), (b - 1, hkv - 1)], f"{splits} split(s)")
+
+
+def test_attn_bwd_wide_long_causal_against_float64_on_device():
+    """B=1, S=4096, Hq=8, Hkv=2, D=256 causal bf16: one kv group's dq / dk / dv against float64 autograd."""
+    b, s, hq, hkv, d = 1, 4096, 8, 2, 256
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    k, v = (torch.randn(b, s, hkv, d, generator=gen, device=DEV).to(torch.bfloat16) for _ in range(2))
+    print("[attn bwd wide] long causal S=4096 D=256", flush=True)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    dq, dk, dv = torch.autograd.grad(impls.attn(*leaves, True), leaves, do)
+    grp = 1  # kv head 1 and its q heads 4..7
+    qh = q[0, :, 4 * grp:4 * grp + 4].double().permute(1, 0, 2).requires_grad_()
+    kh = k[0, :, grp].double().requires_grad_()
+    vh = v[0, :, grp].double().requires_grad_()
+    z = (qh @ kh.T) * d**-0.5
+    z = z.masked_fill(torch.ones(s, s, dtype=torch.bool, device=DEV).triu(1), float("-inf"))
+    o = torch.softmax(z, -1) @ vh
+    gq, gk, gv = torch.autograd.grad(o, (qh, kh, vh), do[0, :, 4 * grp:4 * grp + 4].double().permute(1, 0, 2))
+    for name, got, want in (("dq", dq[0, :, 4 * grp:4 * grp + 4].permute(1, 0, 2), gq), ("dk", dk[0, :, grp], gk),
+                            ("dv", dv[0, :, grp], gv)):
+        err = (got.double() - want).abs().max().item()
+        scale = max(1.0, want.abs().max().item())
+        assert err <= 2e-2 * scale, f"{name}: {err:.3e} vs {scale:.2f}"
