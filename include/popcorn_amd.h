@@ -227,10 +227,10 @@ int pk_qk_norm_rope_bwd(const void* q, const void* k, const void* q_weight, cons
  * o like q; q head h reads kv head h / (q_heads / kv_heads). causal = 1 masks
  * key j > query i (top-left aligned). lse (fp32 [batch, q_heads, seq],
  * natural log) may be NULL. strides[12] = q, k, v, o (batch, seq, head)
- * strides in elements. dtype is PK_BF16 or PK_F16 with head_dim a multiple of
- * 8 up to 256 (rows laid out at 64, 128 or 256 dims, zeros past head_dim), or
- * PK_F32 with head_dim a multiple of 8 up to 128 (the fp32 matrix-core kernel,
- * exact online softmax; strides multiples of 4 elements).
+ * strides in elements. head_dim a multiple of 8 up to 256 (rows laid out at
+ * 64, 128 or 256 dims, zeros past head_dim); dtype PK_BF16, PK_F16, or PK_F32
+ * (the fp32 matrix-core kernel, exact online softmax; strides multiples of 4
+ * elements).
  * Replaces: reference `attn` (kernels/attn.py:10-37,
  * F.scaled_dot_product_attention with enable_gqa=True).
  */
@@ -276,8 +276,8 @@ int64_t pk_attn_bwd_workspace(int64_t batch, int64_t seq, int64_t q_heads, int64
  * (partials of q-head splits are added in a fixed order, so the result is
  * deterministic). strides[24] = q, k, v, o, dout, dq, dk, dv (batch, token,
  * head) strides in elements, multiples of 8 (bf16, fp16) or 4 (fp32).
- * head_dim a multiple of 8 up to 256 (bf16, fp16) or 128 (PK_F32, the fp32
- * matrix-core kernels, v_mfma_f32_32x32x2_f32).
+ * head_dim a multiple of 8 up to 256. dtype PK_BF16, PK_F16 or PK_F32 (the
+ * fp32 matrix-core kernels, v_mfma_f32_32x32x2_f32).
  * Replaces torch autograd of the reference `attn` (kernels/attn.py:30-37).
  */
 int pk_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,

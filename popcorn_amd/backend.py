@@ -136,10 +136,10 @@ def qk_norm_rope_supported(q, k, q_weight, k_weight, cos, sin, eps) -> bool:
     )
 
 
-def _attn_head_dim(head_dim: int, dtype: torch.dtype) -> bool:
-    """head_dim a multiple of 8: up to 256 for the 16-bit kernels and 128 for the fp32 ones, forward and
-    backward alike (so whether autograd records the call does not matter)."""
-    return head_dim % 8 == 0 and 8 <= head_dim <= (256 if dtype in _HALF else 128)
+def _attn_head_dim(head_dim: int) -> bool:
+    """head_dim a multiple of 8 up to 256, in every dtype, forward and backward alike (so whether autograd
+    records the call does not matter)."""
+    return head_dim % 8 == 0 and 8 <= head_dim <= 256
 
 
 def attn_supported(q, k, v, causal, softmax_scale) -> bool:
@@ -147,7 +147,7 @@ def attn_supported(q, k, v, causal, softmax_scale) -> bool:
         _on_hip(q, k, v)
         and q.dtype in _FLOATS
         and q.dtype == k.dtype == v.dtype
-        and _attn_head_dim(q.shape[-1], q.dtype)
+        and _attn_head_dim(q.shape[-1])
         and k.shape[2] > 0
         and q.shape[2] % k.shape[2] == 0
     )
@@ -162,7 +162,7 @@ def attn_varlen_supported(q, k, v, cu_seqlens, causal, softmax_scale) -> bool:
         and q.dtype in _FLOATS
         and q.dtype == k.dtype == v.dtype
         and q.dim() == 3
-        and _attn_head_dim(q.shape[-1], q.dtype)
+        and _attn_head_dim(q.shape[-1])
         and k.shape[1] > 0
         and q.shape[1] % k.shape[1] == 0
     )

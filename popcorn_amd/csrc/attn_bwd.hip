@@ -834,7 +834,7 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + round_up(2 * a.lse_n * (int64_t)sizeof(float)));
   if (dtype != PK_BF16 && dtype != PK_F16 && dtype != PK_F32)
     return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16/fp32 only)", who, dtype);
-  const int64_t max_dim = dtype == PK_F32 ? 128 : 256;
+  const int64_t max_dim = 256;
   if (head_dim <= 0 || head_dim > max_dim || head_dim % 8 != 0)
     return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to %lld)", who, (long long)head_dim,
                 (long long)max_dim);
@@ -870,7 +870,9 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
-  if (dtype == PK_F32) return head_dim <= 64 ? launch_f32<64>(a, causal, s) : launch_f32<128>(a, causal, s);
+  if (dtype == PK_F32)
+    return head_dim <= 64 ? launch_f32<64>(a, causal, s)
+                          : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (head_dim > 128) return dtype == PK_BF16 ? launch_wide<bf16>(a, causal, s) : launch_wide<f16>(a, causal, s);
   if (dtype == PK_BF16) return head_dim <= 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
   return head_dim <= 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);

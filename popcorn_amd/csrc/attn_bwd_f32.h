@@ -17,9 +17,10 @@
 //   accumulations (dQ += dS K, dV^T += dO^T P, dK^T += Q^T dS) contract, at
 //   product t, the row that score register t of the lane holds, so the
 //   score-side operand is register t itself. The result's 32 columns (dQ) or
-//   rows (dV^T, dK^T) at block dt are dims DT j + dt (DT = D / 32), so one
-//   DT-wide read of a row gives product t's operand for every block, and
-//   the DT blocks of an element line up into DT consecutive dims to store.
+//   rows (dV^T, dK^T) at block dt are dims 128 (dt / W) + W j + dt % W
+//   (W = min(D / 32, 4)), so one W-wide read of a row (two at head_dim 256)
+//   gives product t's operand for every block, and the blocks of an element
+//   line up into W consecutive dims to store.
 //
 // Tiles of 32 rows x D dims sit in LDS as unpadded rows of 16-byte chunks,
 // chunk c of row r at c ^ fswz(r) with fswz(r) = (r % 16) ^ 8 ((r / 4) % 2):
@@ -41,34 +42,55 @@ template <int D> __device__ __forceinline__ int fat(int row, int dim) {
   return row * D + (((dim >> 2) ^ fswz(row)) << 2) + (dim & 3);
 }
 
-// The DT floats of a tile row from dim DT * j on, the operand of every block of
-// an accumulation at one product
-template <int DT> struct Span;
-template <> struct Span<4> {
-  float v[4];
-  __device__ __forceinline__ explicit Span(const float* p) {
-    const float4 x = *reinterpret_cast<const float4*>(p);
-    v[0] = x.x;
-    v[1] = x.y;
-    v[2] = x.z;
-    v[3] = x.w;
-  }
+// Accumulation blocks over DO output dims (DO / 32 blocks): block dt's 32
+// result columns (dQ) or rows (dV^T, dK^T) are dims 128 (dt / W) + W j + dt % W
+// with W = min(DO / 32, 4). One W-wide read of a tile row at column W j (and
+// one 128 dims on, for 256 output dims) gives product t's operand for every
+// block, and an element's blocks store as W consecutive dims per 128.
+template <int DO> struct Cols {
+  static constexpr int DT = DO / 32;
+  static constexpr int W = DT < 4 ? DT : 4;
+  static constexpr int NS = DT / W;  // spans, 128 dims apart
 };
-template <> struct Span<2> {
-  float v[2];
+
+// The operands of every block at one product: p is the tile element at column W j of a row (the tile's
+// swizzle keeps a chunk's offset within its 128-dim half, so the second span sits 128 floats on)
+template <int DO> struct Span {
+  using C = Cols<DO>;
+  float v[C::DT];
   __device__ __forceinline__ explicit Span(const float* p) {
-    const float2 x = *reinterpret_cast<const float2*>(p);
-    v[0] = x.x;
-    v[1] = x.y;
+#pragma unroll
+    for (int sp = 0; sp < C::NS; ++sp) {
+      if constexpr (C::W == 4) {
+        const float4 x = *reinterpret_cast<const float4*>(p + 128 * sp);
+        v[4 * sp] = x.x;
+        v[4 * sp + 1] = x.y;
+        v[4 * sp + 2] = x.z;
+        v[4 * sp + 3] = x.w;
+      } else {
+        const float2 x = *reinterpret_cast<const float2*>(p);
+        v[0] = x.x;
+        v[1] = x.y;
+      }
+    }
   }
 };
 
-// DT consecutive floats at p: element r of each block's accumulator, times f
-template <int DT> __device__ __forceinline__ void store_span(float* p, const f32x16 (&acc)[DT], int r, float f) {
-  if constexpr (DT == 4)
-    *reinterpret_cast<float4*>(p) = make_float4(acc[0][r] * f, acc[1][r] * f, acc[2][r] * f, acc[3][r] * f);
-  else
-    *reinterpret_cast<float2*>(p) = make_float2(acc[0][r] * f, acc[1][r] * f);
+// Element r of every block's accumulator, times f, to the W consecutive dims at p (dim `dim` of the row)
+// and, for 256 output dims, 128 dims on; spans from head_dim on are not stored
+template <int DO>
+__device__ __forceinline__ void store_span(float* p, const f32x16 (&acc)[DO / 32], int r, float f, int dim, int dr) {
+  using C = Cols<DO>;
+#pragma unroll
+  for (int sp = 0; sp < C::NS; ++sp) {
+    if (dim + 128 * sp >= dr) continue;
+    const int b0 = C::W * sp;
+    if constexpr (C::W == 4)
+      *reinterpret_cast<float4*>(p + 128 * sp) =
+          make_float4(acc[b0][r] * f, acc[b0 + 1][r] * f, acc[b0 + 2][r] * f, acc[b0 + 3][r] * f);
+    else
+      *reinterpret_cast<float2*>(p) = make_float2(acc[0][r] * f, acc[1][r] * f);
+  }
 }
 
 // Lane offsets (bytes) of the direct loads that fill a 32-row tile: slot
@@ -229,6 +251,8 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
       dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.z, gv[4 * u + 2], dp, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qv[4 * u + 3], s, 0, 0, 0);
       dp = __builtin_amdgcn_mfma_f32_32x32x2f32(vf.w, gv[4 * u + 3], dp, 0, 0, 0);
+      // at 256 dims Q and dO fill the VGPRs: keep the scheduler from hoisting every read ahead
+      if constexpr (D == 256) __builtin_amdgcn_sched_barrier(0);
     }
 
     // dS = P (dP - D) over the keys the row may see
@@ -241,12 +265,13 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
       ds[r] = key > lim ? 0.f : p * (dp[r] - dsum);
     }
 
-    // dQ += dS K: product u takes the key of register u; block dt's column j is dim DT j + dt
+    // dQ += dS K: product u takes the key of register u; block dt's column j is dim 128 (dt / W) + W j + dt % W
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const Span<DT> kd(Kt + fat<D>(8 * (u >> 2) + 4 * g + (u & 3), DT * r32));
+      const Span<D> kd(Kt + fat<D>(8 * (u >> 2) + 4 * g + (u & 3), Cols<D>::W * r32));
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) dq[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[u], kd.v[dt], dq[dt], 0, 0, 0);
+      if constexpr (D == 256) __builtin_amdgcn_sched_barrier(0);
     }
 
     lds_loads_landed();  // this wave's part of the next tile
@@ -254,12 +279,13 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
   }
 
   // dQ = scale dS K: register r of block dt is row 8 (r / 4) + 4 g + r % 4 of the wave, dim DT r32 + dt
-  if (DT * r32 < a.dr) {
-    float* dqb = static_cast<float*>(a.dq) + b * a.dqs[0] + hq * a.dqs[2] + start * a.dqs[1] + DT * r32;
+  {
+    const int col = Cols<D>::W * r32;
+    float* dqb = static_cast<float*>(a.dq) + b * a.dqs[0] + hq * a.dqs[2] + start * a.dqs[1] + col;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = wave_first + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (row < S) store_span<DT>(dqb + (int64_t)row * a.dqs[1], dq, r, a.scale);
+      if (row < S) store_span<D>(dqb + (int64_t)row * a.dqs[1], dq, r, a.scale, col, a.dr);
     }
   }
 }
@@ -430,7 +456,7 @@ void attn_bwd_f32_dkdv_kernel(BwdArgs a) {
       const float* Ct = role == 0 ? Gt : Qt;
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        const Span<DT> cd(Ct + fat<D>(8 * (u >> 2) + 4 * g + (u & 3), DT * r32));
+        const Span<D> cd(Ct + fat<D>(8 * (u >> 2) + 4 * g + (u & 3), Cols<D>::W * r32));
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(cd.v[dt], f[u], acc[dt], 0, 0, 0);
       }
@@ -452,7 +478,193 @@ void attn_bwd_f32_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int i = 8 * (r >> 2) + 4 * g + (r & 3);
-      if (DT * i < a.dr) store_span<DT>(out + DT * i, acc, r, fs);
+      store_span<D>(out + Cols<D>::W * i, acc, r, fs, Cols<D>::W * i, a.dr);
+    }
+  }
+}
+
+// dk/dv kernel at head_dim 256 (and 136-248, laid out at 256). A 32-key slice's
+// K and V half rows alone take 256 registers here and its dK and dV another
+// 256, so one wave per slice does both roles (as the 16-bit kernel at this
+// width) for half of the output dims: block pair (2 w, 2 w + 1) covers the
+// same keys, dims 0-127 and 128-255 of dK and dV, each computing S and dP over
+// all 256 dims (the scores cost twice; the accumulations are split). Per query
+// tile: S = Q K^T and dP = dO V^T interleaved, P and dS in registers, then
+// dV^T += dO^T P and dK^T += Q^T dS over the block's 128 dims. Q/dO tiles are
+// double-buffered.
+template <bool CAUSAL>
+__global__ __attribute__((amdgpu_flat_work_group_size(kF32DqThreads, kF32DqThreads), amdgpu_waves_per_eu(1)))
+void attn_bwd_f32_dkdv_wide_kernel(BwdArgs a) {
+  constexpr int D = 256;
+  constexpr int DO = 128;  // output dims per block
+  constexpr int H = D / 2;
+  constexpr int DT = DO / 32;
+  constexpr int CH = D / 4;
+  constexpr int TILE = BQ * D;
+  constexpr int SLOTS = BQ * CH;
+  constexpr int TI = 2 * SLOTS / kF32DqThreads;  // direct loads per thread per stage: 16 (Q, then dO)
+  static_assert(TI % 2 == 0 && (TI / 2) * kF32DqThreads == SLOTS, "a thread's loads split evenly over Q and dO");
+  __shared__ __attribute__((aligned(16))) float QG[2][2 * TILE];  // buffer: Q tile, then dO tile
+  __shared__ __attribute__((aligned(16))) float RV[2][2][64];     // buffer: lse2 rows, D rows (32 used)
+
+  const int half = blockIdx.x & 1;  // output dims 128 half .. 128 half + 127
+  const int w = blockIdx.x >> 1;
+  const int per_tile = a.B * a.Hkv * a.nsplit;
+  const int kv_tile = w / per_tile;  // first key tiles (the most causal work) first
+  const int gi = w % per_tile;
+  const int b = gi / (a.Hkv * a.nsplit);
+  const int hkv = (gi / a.nsplit) % a.Hkv;
+  const int split = gi % a.nsplit;
+  const int heads = a.group / a.nsplit;
+  int start, S;
+  seq_bounds(a, b, start, S);
+  const int kb0 = kv_tile * BK;
+  if (kb0 >= S || 128 * half >= a.dr) return;  // whole block, before any barrier
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int r32 = lane & 31;
+  const int g = lane >> 5;
+  const int kw0 = kb0 + wave * 32;
+  const int key = kw0 + r32;
+  const bool key_ok = key < S;
+
+  // the lane's K and V half rows (dims H g + t)
+  float kv[H], vv[H];
+  {
+    const float* krow = static_cast<const float*>(a.k) + b * a.ks[0] + hkv * a.ks[2] + (int64_t)(start + key) * a.ks[1];
+    const float* vrow = static_cast<const float*>(a.v) + b * a.vs[0] + hkv * a.vs[2] + (int64_t)(start + key) * a.vs[1];
+#pragma unroll
+    for (int u = 0; u < H / 4; ++u) {
+      const int d = H * g + 4 * u;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+      if (key_ok && d < a.dr) {
+        x = *reinterpret_cast<const float4*>(krow + d);
+        y = *reinterpret_cast<const float4*>(vrow + d);
+      }
+      kv[4 * u] = x.x;
+      kv[4 * u + 1] = x.y;
+      kv[4 * u + 2] = x.z;
+      kv[4 * u + 3] = x.w;
+      vv[4 * u] = y.x;
+      vv[4 * u + 1] = y.y;
+      vv[4 * u + 2] = y.z;
+      vv[4 * u + 3] = y.w;
+    }
+  }
+  const float cs = a.q_flip ? -a.c : a.c;  // Q is staged unflipped
+
+  const int u0 = CAUSAL ? kb0 / BQ : 0;
+  const int n_u = (S + BQ - 1) / BQ - u0;
+  const int n_it = heads * n_u;
+
+  int go[TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+    go[i] = tile_offset<D>((i * kF32DqThreads + tid) % SLOTS, i < TI / 2 ? a.qs[1] : a.gs[1], a.dr);
+  auto issue = [&](int it, int st) {
+    const int hq = hkv * a.group + split * heads + it / n_u;
+    const int r0 = (u0 + it % n_u) * BQ;
+    const float* qb = static_cast<const float*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
+    const float* gb = static_cast<const float*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
+    const __amdgpu_buffer_rsrc_t qrs = rows_rsrc(qb, S, a.qs[1], a.dr);
+    const __amdgpu_buffer_rsrc_t grs = rows_rsrc(gb, S, a.gs[1], a.dr);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+      ld_buf_lds(i < TI / 2 ? qrs : grs, &QG[st][(i * kF32DqThreads + wave * 64) * 4], go[i],
+                 r0 * (int)(i < TI / 2 ? a.qs[1] : a.gs[1]) * (int)sizeof(float));
+    if (wave < 2) {
+      const float* rb = a.dsum + b * a.lse_bs + hq * a.lse_hs + start + (wave == 0 ? a.lse_n : 0);
+      const __amdgpu_buffer_rsrc_t rrs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)rb, (short)0, S * (int)sizeof(float), 0x00020000);
+      ld_buf_lds4(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
+    }
+  };
+
+  f32x16 acc_v[DT], acc_k[DT];  // dV^T and dK^T over the block's dims: block dt's row i is dim 128 half + 4 i + dt
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_v[dt][r] = acc_k[dt][r] = 0.f;
+
+  issue(0, 0);
+  lds_loads_landed();
+  __syncthreads();
+  for (int t = 0; t < n_it; ++t) {
+    const int st = t & 1;
+    if (t + 1 < n_it) issue(t + 1, st ^ 1);
+    const float* Qt = QG[st];
+    const float* Gt = QG[st] + TILE;
+    const int r0 = (u0 + t % n_u) * BQ;
+
+    // S = Q K^T and dP = dO V^T over all 256 dims: register r holds query row r0 + 8 (r / 4) + 4 g + r % 4
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+    for (int u = 0; u < H / 4; ++u) {
+      const float4 qf = *reinterpret_cast<const float4*>(Qt + fat<D>(r32, H * g + 4 * u));
+      const float4 gf = *reinterpret_cast<const float4*>(Gt + fat<D>(r32, H * g + 4 * u));
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf.x, kv[4 * u], s, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(gf.x, vv[4 * u], dp, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf.y, kv[4 * u + 1], s, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(gf.y, vv[4 * u + 1], dp, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf.z, kv[4 * u + 2], s, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(gf.z, vv[4 * u + 2], dp, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(qf.w, kv[4 * u + 3], s, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x2f32(gf.w, vv[4 * u + 3], dp, 0, 0, 0);
+    }
+
+    // P = exp2(s c - lse2), dS = P (dP - D); masked rows and keys get 0
+    float p[16], ds[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 l4 = *reinterpret_cast<const float4*>(&RV[st][0][8 * j + 4 * g]);
+      const float4 d4 = *reinterpret_cast<const float4*>(&RV[st][1][8 * j + 4 * g]);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * j + i;
+        const int qr = r0 + 8 * j + 4 * g + i;
+        const bool masked = qr >= S || (CAUSAL && qr < key);
+        p[r] = masked ? 0.f : exp2f(fmaf(s[r], cs, -lv[i]));
+        ds[r] = masked ? 0.f : p[r] * (dp[r] - dv[i]);
+      }
+    }
+
+    // dV^T += dO^T P and dK^T += Q^T dS over dims 128 half + 4 i + dt: product u takes the query row of register u
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int row = 8 * (u >> 2) + 4 * g + (u & 3);
+      const Span<DO> gd(Gt + fat<D>(row, 128 * half + 4 * r32));
+      const Span<DO> qd(Qt + fat<D>(row, 128 * half + 4 * r32));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        acc_v[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(gd.v[dt], p[u], acc_v[dt], 0, 0, 0);
+        acc_k[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(qd.v[dt], ds[u], acc_k[dt], 0, 0, 0);
+      }
+    }
+
+    lds_loads_landed();  // this wave's part of the next tile
+    __syncthreads();
+  }
+
+  if (key_ok) {
+    float *dv_out, *dk_out;
+    if (a.nsplit > 1) {  // fp32 partials of this block's heads; dkdv_sum_kernel adds the splits
+      const int64_t row = (a.cu != nullptr ? (int64_t)start : (int64_t)b * a.S) + key;
+      dv_out = a.part + (((int64_t)(split * 2 + 0) * a.rows + row) * a.Hkv + hkv) * D;
+      dk_out = a.part + (((int64_t)(split * 2 + 1) * a.rows + row) * a.Hkv + hkv) * D;
+    } else {
+      dv_out = static_cast<float*>(a.dv) + b * a.dvs[0] + hkv * a.dvs[2] + (int64_t)(start + key) * a.dvs[1];
+      dk_out = static_cast<float*>(a.dk) + b * a.dks[0] + hkv * a.dks[2] + (int64_t)(start + key) * a.dks[1];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 128 * half + 4 * (8 * (r >> 2) + 4 * g + (r & 3));
+      store_span<DO>(dv_out + d, acc_v, r, 1.0f, d, a.dr);
+      store_span<DO>(dk_out + d, acc_k, r, a.scale, d, a.dr);  // signed scale: Q was staged unflipped
     }
   }
 }
@@ -461,11 +673,18 @@ template <int D> int launch_f32(const BwdArgs& a, bool causal, hipStream_t s) {
   const int gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
   const int64_t dq_blocks = (int64_t)((a.S + 32 * (4 / gp) - 1) / (32 * (4 / gp))) * a.B * a.Hq / gp;
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv * a.nsplit;
-  if (causal) {
+  if (causal)
     hipLaunchKernelGGL((attn_bwd_f32_dq_kernel<D, true>), dim3(dq_blocks), dim3(kF32DqThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_bwd_f32_dq_kernel<D, false>), dim3(dq_blocks), dim3(kF32DqThreads), 0, s, a);
+  if constexpr (D == 256) {  // two blocks per 128 keys, one per half of the output dims
+    if (causal)
+      hipLaunchKernelGGL((attn_bwd_f32_dkdv_wide_kernel<true>), dim3(2 * kv_blocks), dim3(kF32DqThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((attn_bwd_f32_dkdv_wide_kernel<false>), dim3(2 * kv_blocks), dim3(kF32DqThreads), 0, s, a);
+  } else if (causal) {
     hipLaunchKernelGGL((attn_bwd_f32_dkdv_kernel<D, true>), dim3(kv_blocks), dim3(kF32DkdvThreads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_f32_dq_kernel<D, false>), dim3(dq_blocks), dim3(kF32DqThreads), 0, s, a);
     hipLaunchKernelGGL((attn_bwd_f32_dkdv_kernel<D, false>), dim3(kv_blocks), dim3(kF32DkdvThreads), 0, s, a);
   }
   if (a.nsplit > 1) {

@@ -470,7 +470,7 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
                 (long long)kv_heads);
   if (dtype != PK_BF16 && dtype != PK_F16 && dtype != PK_F32)
     return fail(PK_ERR_UNSUPPORTED, "%s: dtype code %d (bf16/fp16/fp32 only)", who, dtype);
-  const int max_dim = dtype == PK_F32 ? 128 : 256;
+  const int max_dim = 256;
   if (head_dim <= 0 || head_dim > max_dim || head_dim % 8 != 0)
     return fail(PK_ERR_UNSUPPORTED, "%s: head_dim=%lld (a multiple of 8 up to %d for this dtype)", who,
                 (long long)head_dim, max_dim);
@@ -516,7 +516,9 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
   // rows are laid out at 64, 128 or 256 dims, the chunks past head_dim reading as zeros
-  if (dtype == PK_F32) return head_dim <= 64 ? launch_f32<64>(a, causal, s) : launch_f32<128>(a, causal, s);
+  if (dtype == PK_F32)
+    return head_dim <= 64 ? launch_f32<64>(a, causal, s)
+                          : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (dtype == PK_BF16)
     return head_dim <= 64 ? launch<bf16, 64>(a, causal, s)
                           : head_dim <= 128 ? launch<bf16, 128>(a, causal, s) : launch<bf16, 256>(a, causal, s);

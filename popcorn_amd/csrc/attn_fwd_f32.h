@@ -26,8 +26,9 @@
 
 constexpr int kF32Threads = 256;
 
+// head_dim 256 holds Q's half row and the O^T accumulator in 256 registers: one wave per SIMD
 template <int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(kF32Threads, kF32Threads), amdgpu_waves_per_eu(2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kF32Threads, kF32Threads), amdgpu_waves_per_eu(D == 256 ? 1 : 2)))
 void attn_fwd_f32_kernel(AttnArgs a) {
   constexpr int H = D / 2;                    // dims per half-wave in the score contraction
   constexpr int DT = D / 32;                  // 32-dim blocks of O^T

@@ -631,11 +631,10 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
 
 
 def _grad_supported(op: str, head_dim: int, dtype: torch.dtype) -> None:
-    """Refuse, before any work, a call whose backward the kernels do not cover: head_dim above 256 (16-bit)
-    or 128 (fp32), where the forward kernels stop too."""
-    widest = 256 if dtype in _HALF else 128
-    if head_dim > widest:
-        raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} is past the {dtype} kernels' {widest}")
+    """Refuse, before any work, a call whose backward the kernels do not cover: head_dim above 256, where
+    the forward kernels stop too."""
+    if head_dim > 256:
+        raise ValueError(f"popcorn_amd.{op}: head_dim={head_dim} is past the attention kernels' 256")
 
 
 def _scale(head_dim: int, softmax_scale: float | None) -> float:

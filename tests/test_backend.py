@@ -99,7 +99,7 @@ def test_attention_predicates_cover_the_head_dims(monkeypatch):
 
 
 def test_attention_predicates_take_fp32(monkeypatch):
-    """fp32 attention runs the fp32 kernels, head_dim up to 128, with or without gradients to record."""
+    """fp32 attention runs the fp32 kernels, head_dim up to 256, with or without gradients to record."""
     monkeypatch.setattr(backend, "_on_hip", lambda *tensors: True)
 
     def qkv(d, grad=False):
@@ -107,12 +107,12 @@ def test_attention_predicates_take_fp32(monkeypatch):
         k = torch.empty(1, 16, 2, d, dtype=torch.float32, device="meta")
         return [t.requires_grad_(grad) for t in (q, k, k.clone())]
 
-    for d in (16, 32, 64, 96, 128):
+    for d in (16, 32, 64, 96, 128, 192, 256):
         assert backend.attn_supported(*qkv(d), True, None)
         assert backend.attn_supported(*qkv(d, grad=True), True, None)
         q, k, v = (t[0] for t in qkv(d, grad=True))
         assert backend.attn_varlen_supported(q, k, v, torch.zeros(2, dtype=torch.int32), False, None)
-    for d in (192, 256, 100):
+    for d in (264, 100, 4):
         assert not backend.attn_supported(*qkv(d), True, None)
         assert not backend.attn_supported(*qkv(d, grad=True), True, None)
 
@@ -120,8 +120,8 @@ def test_attention_predicates_take_fp32(monkeypatch):
 def test_attention_with_gradients_past_the_kernels_is_refused_before_any_work():
     from popcorn_amd import impls
 
-    for q, what in ((torch.randn(1, 4, 2, 192, requires_grad=True), "head_dim=192 is past the torch.float32"),
-                    (torch.randn(1, 4, 2, 264).bfloat16().requires_grad_(), "head_dim=264 is past the torch.bfloat16")):
+    for q in (torch.randn(1, 4, 2, 264, requires_grad=True), torch.randn(1, 4, 2, 264).bfloat16().requires_grad_()):
+        what = "head_dim=264 is past the attention kernels' 256"
         # CPU tensors: the refusal comes first
         for call in (lambda: impls.attn(q, q, q, True),
                      lambda: impls.attn_varlen(q[0], q[0], q[0], torch.tensor([0, 4]))):

@@ -61,16 +61,17 @@ def _check(batch, seq, hq, hkv, d, causal, scale, seed=0):
         gauge_ok(got, want, r, F32, f"{name} (seq {seq}, d {d}, causal {causal}, scale {scale})")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("seq", [1, 17, 64, 130, 257])
 def test_attn_bwd_f32_shapes(seq, causal, d):
     _check(2, seq, 8, 2, d, causal, None)
 
 
-@pytest.mark.parametrize("d", [16, 40, 96, 120])
+@pytest.mark.parametrize("d", [16, 40, 96, 120, 136, 192, 248])
 def test_attn_bwd_f32_head_dims_laid_out_wider(d):
-    """head_dim below the 64- or 128-dim layout: the dims past it read as zeros and are never stored."""
+    """head_dim below the 64-, 128- or 256-dim layout: the dims past it read as zeros and are never stored
+    (at 136 the second half of the dk/dv output dims is a block that stores nothing past 136)."""
     _check(1, 77, 4, 1, d, True, None, seed=4)
 
 
@@ -80,10 +81,16 @@ def test_attn_bwd_f32_groups(heads, causal):
     _check(2, 150, heads[0], heads[1], 64 if heads[0] % 3 == 0 else 128, causal, None, seed=11)
 
 
+@pytest.mark.parametrize("heads", [(8, 1), (6, 2)], ids=str)
+def test_attn_bwd_f32_wide_groups(heads):
+    _check(2, 130, heads[0], heads[1], 256, True, None, seed=13)
+
+
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("scale", [0.25, -0.3, 1e-3])
-def test_attn_bwd_f32_scales(scale):
+def test_attn_bwd_f32_scales(scale, d):
     """A negative scale negates q on load in the dq kernel and signs the exponent in the dk/dv kernel."""
-    _check(1, 96, 4, 2, 128, False, scale, seed=9)
+    _check(1, 96, 4, 2, d, False, scale, seed=9)
 
 
 def test_attn_bwd_f32_noncontiguous_inputs_and_cotangent():
@@ -100,11 +107,12 @@ def test_attn_bwd_f32_noncontiguous_inputs_and_cotangent():
         assert torch.equal(a, b_)
 
 
+@pytest.mark.parametrize("d", [128, 256])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("total,segments", [(37, 1), (300, 3), (129, 129)])
-def test_attn_varlen_bwd_f32(total, segments, causal):
+def test_attn_varlen_bwd_f32(total, segments, causal, d):
     cu = R.cuts(torch.zeros(segments + 1, dtype=torch.int64), {"total": total}, torch.Generator().manual_seed(0))
-    hq, hkv, d = 8, 2, 128
+    hq, hkv = 8, 2
     q = seeded((total, hq, d), 0, F32)
     k = seeded((total, hkv, d), 1, F32)
     v = seeded((total, hkv, d), 2, F32)
@@ -144,12 +152,15 @@ def _splits(ws_bytes, lse_n, rows, hkv, d):
     (4, 1024, 32, 16, 64, True, 1),    # 512 blocks: direct, two q heads per block
     (8, 1024, 32, 8, 128, False, 1),   # 512 blocks: direct, four q heads per block
     (4, 1024, 32, 8, 128, True, 2),    # 256 blocks: two splits of two q heads
-], ids=["direct-d64-causal", "direct-d128-full", "split2-d128-causal"])
+    (8, 1024, 32, 8, 256, True, 1),    # 512 key blocks (1024 dk/dv blocks, two per 128 keys): direct
+    (2, 1024, 16, 2, 192, False, 8),   # 32 key blocks, group 8: one q head per block
+], ids=["direct-d64-causal", "direct-d128-full", "split2-d128-causal", "direct-d256-causal", "split8-d192-full"])
 def test_attn_bwd_f32_dkdv_direct_and_partial_splits(b, s, hq, hkv, d, causal, splits):
     """Full-size grids on each dk/dv path; sampled (batch, kv group) slices against the float64 oracle (a kv
     group's gradients depend only on its own q heads, so a slice is an exact subproblem)."""
     lib = _lib.load()
-    assert _splits(lib.pk_attn_bwd_workspace(b, s, hq, hkv, d), b * hq * s, b * s, hkv, d) == splits
+    width = 64 if d <= 64 else (128 if d <= 128 else 256)
+    assert _splits(lib.pk_attn_bwd_workspace(b, s, hq, hkv, d), b * hq * s, b * s, hkv, width) == splits
     print(f"[attn bwd f32] grid b={b} s={s} hq={hq} hkv={hkv} d={d} causal={causal} splits={splits}", flush=True)
     gen = torch.Generator(device=DEV).manual_seed(17)
     q, do = (torch.randn(b, s, hq, d, generator=gen, device=DEV) for _ in range(2))

@@ -61,16 +61,16 @@ def _check(batch, seq, hq, hkv, d, causal, scale, seed=0, views=False):
     return om
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("seq", [1, 17, 64, 200, 257])
 def test_attn_f32_shapes(seq, causal, d):
     _check(2, seq, 8, 2, d, causal, None)
 
 
-@pytest.mark.parametrize("d", [16, 32, 48, 80, 96, 120])
+@pytest.mark.parametrize("d", [16, 32, 48, 80, 96, 120, 136, 192, 248])
 def test_attn_f32_head_dims_laid_out_wider(d):
-    """head_dim below the 64- or 128-dim layout: the dims past it read as zeros and are never stored."""
+    """head_dim below the 64-, 128- or 256-dim layout: the dims past it read as zeros and are never stored."""
     _check(1, 77, 4, 1, d, True, None, seed=4)
 
 
@@ -159,3 +159,8 @@ def test_attn_f32_long_sequence_sampled_rows():
         ref = torch.nn.functional.scaled_dot_product_attention(qh[rows][None], kh[None], vh[None], attn_mask=mask[None])[0]
         gauge_ok(o[0, rows, h], o64, ref, F32, f"o[0,:,{h}]")
         np.testing.assert_allclose(lse[0, h, rows].cpu().double().numpy(), lse64, rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize("heads", [(8, 1), (6, 2)], ids=str)
+def test_attn_f32_wide_groups(heads):
+    _check(2, 130, heads[0], heads[1], 256, True, None, seed=13)
