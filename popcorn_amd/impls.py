@@ -620,9 +620,8 @@ def attn(q: Tensor, k: Tensor, v: Tensor, causal: bool = False, softmax_scale: f
     """softmax(q k^T * scale + causal mask) v with grouped kv heads.
 
     q [batch, seq, q_heads, head_dim], k, v [batch, seq, kv_heads, head_dim];
-    bf16 or fp16 with head_dim a multiple of 8 up to 256 (up to 128 with
-    gradients), or fp32 up to 128 (forward only); scale defaults to
-    head_dim ** -0.5. Backward gives dq, dk, dv.
+    bf16, fp16 or fp32 with head_dim a multiple of 8 up to 256; scale
+    defaults to head_dim ** -0.5. Backward gives dq, dk, dv.
     """
     if _tracks_grad(q, k, v):
         _grad_supported("attn", q.shape[-1], q.dtype)
