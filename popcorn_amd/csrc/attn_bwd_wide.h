@@ -17,10 +17,10 @@
 
 constexpr int kWideThreads = 256;  // four 32-key slices, one wave each
 
-template <typename T, bool CAUSAL>
+template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWideThreads, kWideThreads), amdgpu_waves_per_eu(1)))
 void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
-  constexpr int D = 256;
+  static_assert(D == 128 || D == 256, "rows of 128 or 256 dims");
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
   constexpr int KCH = D / 8;                    // 16-byte chunks per row
@@ -111,26 +111,28 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
     }
   };
 
-  // Lane offsets of the fragment reads. Chunks 16 .. 31 of a row keep their
-  // swizzle 16 chunks on, so the second half of the row (h >= 8, dt >= 4) is
-  // the first half's offset plus 128 elements.
-  int a_lane[KK / 2], t_lane[2][DT / 2];
+  // Lane offsets of the fragment reads. At 256 dims chunks 16 .. 31 of a row
+  // keep their swizzle 16 chunks on, so the second half of the row (h >= 8,
+  // dt >= 4) is the first half's offset plus 128 elements.
+  constexpr int HALVES = D / 128;
+  constexpr int KH = KK / HALVES, DH = DT / HALVES;
+  int a_lane[KH], t_lane[2][DH];
 #pragma unroll
-  for (int h = 0; h < KK / 2; ++h) a_lane[h] = L::at(r32, 16 * h + 8 * g);
+  for (int h = 0; h < KH; ++h) a_lane[h] = L::at(r32, 16 * h + 8 * g);
 #pragma unroll
   for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
-    for (int dt = 0; dt < DT / 2; ++dt)
+    for (int dt = 0; dt < DH; ++dt)
       t_lane[hi][dt] = L::at(8 * hi + 4 * g + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
   // row fragment h of a tile (A operand of a score product: its 32 rows, dims 16 h + 8 g ..)
   auto row_frag = [&](const T* tile, int h) -> Frag {
-    return *reinterpret_cast<const Frag*>(tile + a_lane[h % (KK / 2)] + (h / (KK / 2)) * 128);
+    return *reinterpret_cast<const Frag*>(tile + a_lane[h % KH] + (h / KH) * 128);
   };
   // transposed fragment of a tile (A operand of an accumulation: dims 32 dt + row l % 32, rows of chunk c)
   auto col_frag = [&](const T* tile, int c, int dt) -> Frag {
-    const int off = 16 * c * L::ST + (dt / (DT / 2)) * 128;
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[0][dt % (DT / 2)] + off));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[1][dt % (DT / 2)] + off));
+    const int off = 16 * c * L::ST + (dt / DH) * 128;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[0][dt % DH] + off));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[1][dt % DH] + off));
     return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
@@ -202,12 +204,12 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
       }
     }
 
-    // dV^T += dO^T P and dK^T += Q^T dS: product 2h (h = 8 c + dt) accumulates block dt of dV^T over the 16
+    // dV^T += dO^T P and dK^T += Q^T dS: product 2h (h = DT c + dt) accumulates block dt of dV^T over the 16
     // query rows of fragment c, 2h + 1 the same block of dK^T
     run(
-        [&](int i) { return col_frag(i & 1 ? Qt : Gt, i >> 4, (i >> 1) & 7); },
+        [&](int i) { return col_frag(i & 1 ? Qt : Gt, (i >> 1) / DT, (i >> 1) % DT); },
         [&](int i, const Frag& f) {
-          const int dt = (i >> 1) & 7, c = i >> 4;
+          const int dt = (i >> 1) % DT, c = (i >> 1) / DT;
           if (i & 1)
             acc_k[dt] = Mma<T>::run(f, sf[c], acc_k[dt]);
           else
@@ -264,10 +266,10 @@ template <typename T> int launch_wide(const BwdArgs& a, bool causal, hipStream_t
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv * a.nsplit;
   if (causal) {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, 256, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, true>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, 256, true>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
   } else {
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, 256, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, false>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, 256, false>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
   }
   if (a.nsplit > 1) {
     const int64_t n = a.rows * a.Hkv * (a.dr / 4);
