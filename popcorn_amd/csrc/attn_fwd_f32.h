@@ -96,21 +96,25 @@ void attn_fwd_f32_kernel(AttnArgs a) {
   const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
-  // ---- staging: chunk i = j * 256 + tid of a tile is key i / CH, dims 4 (i % CH) .. + 3
-  float4 kreg[PER], vreg[PER];
-  auto fetch = [&](int tile) {
+  // ---- staging: chunk i = j * 256 + tid of a tile is key i / CH, dims 4 (i % CH) .. + 3. At 256 dims a
+  // tile goes through the registers in two parts (one staged after the scores, one after the step), so
+  // the staging holds 32 registers instead of 64.
+  constexpr int PARTS = D == 256 ? 2 : 1;
+  constexpr int PP = PER / PARTS;  // chunks per thread per part
+  float4 kreg[PP], vreg[PP];
+  auto fetch = [&](int tile, int part) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = j * kF32Threads + tid, key = tile * BN + i / CH, d = 4 * (i % CH);
+    for (int j = 0; j < PP; ++j) {
+      const int i = (part * PP + j) * kF32Threads + tid, key = tile * BN + i / CH, d = 4 * (i % CH);
       const bool ok = key < S && d < a.dr;
       kreg[j] = ok ? *reinterpret_cast<const float4*>(kbase + (int64_t)key * a.kss + d) : make_float4(0.f, 0.f, 0.f, 0.f);
       vreg[j] = ok ? *reinterpret_cast<const float4*>(vbase + (int64_t)key * a.vss + d) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, int part) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = j * kF32Threads + tid, key = i / CH, d = 4 * (i % CH);
+    for (int j = 0; j < PP; ++j) {
+      const int i = (part * PP + j) * kF32Threads + tid, key = i / CH, d = 4 * (i % CH);
       *reinterpret_cast<float4*>(&Ks[buf][key * KST + d]) = kreg[j];
       Vt[buf][(d + 0) * VST + key] = vreg[j].x;
       Vt[buf][(d + 1) * VST + key] = vreg[j].y;
@@ -127,12 +131,15 @@ void attn_fwd_f32_kernel(AttnArgs a) {
   float m = -INFINITY, l = 0.f;  // the row's running max (exp2 domain) and sum; both halves of the wave hold them
   const float c = a.c;
 
-  fetch(0);
-  stage(0);
+#pragma unroll
+  for (int part = 0; part < PARTS; ++part) {
+    fetch(0, part);
+    stage(0, part);
+  }
   __syncthreads();
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < n_tiles) fetch(t + 1);
+    if (t + 1 < n_tiles) fetch(t + 1, 0);
 
     // S^T = K Q^T: score register r holds key 8 (r / 4) + 4 g + r % 4 of this tile for the lane's row
     f32x16 s;
@@ -146,6 +153,15 @@ void attn_fwd_f32_kernel(AttnArgs a) {
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qv[4 * u + 1], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qv[4 * u + 2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qv[4 * u + 3], s, 0, 0, 0);
+    }
+
+    // two-part staging: the first part of the next tile into the other buffer (nothing reads it this
+    // step), then the second part's loads, in flight over the rest of the step
+    if constexpr (PARTS == 2) {
+      if (t + 1 < n_tiles) {
+        stage(buf ^ 1, 0);
+        fetch(t + 1, 1);
+      }
     }
 
     // online softmax over the tile's keys a row may see
@@ -190,7 +206,7 @@ void attn_fwd_f32_kernel(AttnArgs a) {
     }
 
     // the next tile into the other buffer, which every wave finished reading in the last step
-    if (t + 1 < n_tiles) stage(buf ^ 1);
+    if (t + 1 < n_tiles) stage(buf ^ 1, PARTS - 1);
     __syncthreads();
   }
 
