@@ -26,7 +26,10 @@ record-driven selector compares against. `cpu_baseline` times that reference
 on the host's cores, on the full workload where it takes seconds and on a
 stated sample otherwise. `others` holds the same figures for the remaining
 configs, and `roofline_fractions` the dominant kernels' fractions of peak for
-C1-C5.
+C1-C5. In the default run each `roofline` also carries `ceiling`: the probe of
+the same pattern (reads per write and bytes, or the matrix-core rate with the
+attention forward's vector work) timed on the same box after every workload,
+and the kernel's rate as a share of it.
 """
 
 from __future__ import annotations
@@ -706,6 +709,42 @@ def _roofline(wl: Workload, steps: int, warmup: int) -> dict:
     }
 
 
+# The ceiling each dominant kernel is compared against in the same run: the streaming probe with
+# the kernel's reads per write and bytes (pk_probe_stream, rotated like C1), or the matrix-core probe
+# with the forward's per-score vector work (pk_probe_mfma). add_rmsnorm's backward reads three
+# streams, a pattern the probe does not have; the attention backward's vector work differs from the
+# forward's, so it gets none either.
+CEILINGS = {
+    "c1": "stream_1r_64m",      # x [4096, 4096] fp32 in, y out
+    "c2": "stream_2r_448m",     # a, b [16384, 14336] bf16 in, y out
+    "c3": "stream_1r_256m",     # the q call: q [8, 4096, 32, 128] bf16 in and out
+    "c4": "stream_2r_1024m",    # the backward call: x, dy [65536, 8192] bf16 in, dx out
+    "c5": "mfma_ceiling_softmax",
+    "rope": "stream_1r_160m",   # q and k in, their rotations out
+    "qk_norm_rope": "stream_2r_160m",  # the backward: q/k and their cotangents in, gradients out
+}
+
+
+def _ceiling(name: str, dev: torch.device, kernel_rate: float, steps: int) -> dict | None:
+    """The same-run ceiling of workload `name`'s dominant kernel: the probe's launch time and rate, and
+    the kernel's rate as a share of it (the kernel's distance from what its pattern can reach on this
+    box, as opposed to the published peak)."""
+    probe = CEILINGS.get(name)
+    if probe is None:
+        return None
+    torch.cuda.empty_cache()
+    wl = make_workload(probe, dev)
+    reps = _reps(wl.launch, max(5, steps))
+    avg = _time_gpu(wl.launch, reps, _reps(wl.launch, 2, target_ms=60.0)) / reps
+    rate = _rate(wl.kernel_work, avg, wl.unit)
+    hbm = wl.unit == "TB/s"
+    out = {"probe": probe, "avg_launch_us": round(avg * 1e3, 2), "achieved": round(rate * (1000 if hbm else 1), 2),
+           "unit": "GB/s" if hbm else "TFLOP/s", "kernel_share": round(kernel_rate / rate, 4)}
+    del wl
+    torch.cuda.empty_cache()
+    return out
+
+
 def _cpu_threads() -> tuple[int, int]:
     """(threads to use, cores this process may run on): every core of the affinity mask, within the
     host's CPU share for this GPU when one is set (OMP_NUM_THREADS on the GPU boxes)."""
@@ -791,6 +830,7 @@ def main(argv=None) -> int:
         print(f"bench: torch on the GPU {torch_gpu['ms_per_step']} ms/step ({torch_gpu['speedup']}x)", file=sys.stderr,
               flush=True)
     head_unit, head_dtype, head_config = wl.unit, wl.dtype, {"workload": wl.description, **wl.config}
+    head_default = args.head_dim == 128  # the ceilings are taken at the BASELINE head_dim
     others = {}
     if not args.no_others and args.workload in ("c1", "c2", "c3", "c4", "c5", "attn_bwd", "add_rmsnorm", "rope",
                                                  "qk_norm_rope"):
@@ -815,6 +855,17 @@ def main(argv=None) -> int:
                   file=sys.stderr, flush=True)
             del wl_o
         torch.cuda.empty_cache()
+        # the ceilings run after every workload's own figures, so no workload is timed right after a probe
+        for name, rf in [(args.workload, roof if head_default else None),
+                         *((n, o["roofline"]) for n, o in others.items())]:
+            if rf is None:
+                continue
+            rate = rf["achieved"] / (1000 if rf["unit"] == "GB/s" else 1)
+            ceiling = _ceiling(name, dev, rate, args.steps)
+            if ceiling is not None:
+                rf["ceiling"] = ceiling
+                print(f"bench: {name} ceiling {ceiling['probe']} {ceiling['avg_launch_us']} us, kernel at "
+                      f"{ceiling['kernel_share']} of it", file=sys.stderr, flush=True)
     else:
         del wl
     # The CPU baselines run after every GPU figure is taken, so the host threads they leave busy
