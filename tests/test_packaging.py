@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import json
 import os
+import shutil
 import subprocess
 import sys
 from pathlib import Path
@@ -43,9 +44,17 @@ def test_the_distribution_installs_offline_and_its_gate_resolves(tmp_path):
     if not _lib.LIBRARY.exists():
         pytest.fail(f"{_lib.LIBRARY} is not built; run __graft_entry__.build()")
     target = tmp_path / "site"
+    # installed from a copy of the distribution's files, so setuptools' build directory lands there and
+    # not in the source tree
+    src = tmp_path / "src"
+    src.mkdir()
+    for name in ("setup.py", "README.md"):
+        shutil.copy2(ROOT / name, src / name)
+    shutil.copytree(ROOT / "popcorn_amd", src / "popcorn_amd",
+                    ignore=shutil.ignore_patterns("__pycache__", "_build", "*.pyc"))
     env = {**os.environ, "POPCORN_AMD_PREBUILT": "1", "PIP_NO_INDEX": "1", "PIP_DISABLE_PIP_VERSION_CHECK": "1"}
     install = subprocess.run([sys.executable, "-m", "pip", "install", "--no-deps", "--no-build-isolation",
-                              "--target", str(target), str(ROOT)], env=env, capture_output=True, text=True,
+                              "--target", str(target), str(src)], env=env, capture_output=True, text=True,
                              timeout=600)
     assert install.returncode == 0, install.stdout[-2000:] + install.stderr[-2000:]
     assert (target / "popcorn_amd" / "libpopcorn_amd.so").exists()
