@@ -47,14 +47,16 @@
 // 64 consecutive slots, each lane fetching the chunk its slot holds, and a
 // lane whose K slot is padding reads past the buffer's range, which returns
 // zeros without a memory access):
-//   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272
-//       (or 144) bytes apart and so cover all 64 banks once.
+//   K [BN][D + 8]: 16-byte fragment reads of 16 consecutive rows start 272,
+//       208 or 144 bytes apart and so cover all 64 banks once.
 //   V [BN][D], unpadded, with chunk c of row r at slot c ^ vswz(r). V^T
 //       fragments come from ds_read_b64_tr_b16: within a 16-lane group, lane
 //       s reads keys base + s/4, dims d0 + 4*(s%4) .. +3, and lane i receives
 //       dims d0 + i of keys base .. base + 3 -- half of one MFMA A fragment.
 //       The two 16-lane groups served together read 4 rows x 4 chunks, which
 //       the swizzle places in 16 distinct slots of a 256-byte bank window.
+//       96-dim rows (192 bytes) need no swizzle: 4 consecutive rows start 0,
+//       192, 128 and 64 bytes into that window.
 //
 // K and V are read through buffer resources based at the (batch, kv head):
 // a tile is one scalar offset, and rows at or past S read as zero, so no load
@@ -85,8 +87,12 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 
 // Slot of chunk c of V row r is c ^ vswz(r): the two 16-lane groups of a
 // transposing read cover 4 rows x 4 chunks, which this spreads over 16
-// distinct slots of a 256-byte bank window (rows of head_dim 64 are 128 bytes).
-template <int D> __device__ __forceinline__ int vswz(int r) { return D >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+// distinct slots of a 256-byte bank window (rows of head_dim 64 are 128 bytes;
+// 96-dim rows, 192 bytes, already start 64 bytes apart modulo the window).
+template <int D> __device__ __forceinline__ int vswz(int r) {
+  if constexpr (D == 96) return 0;
+  else return D >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
 
 // Largest row sum the fixed-max sweep accepts (see the header).
 template <typename T> constexpr float kFastLimit = 4294967296.0f;
@@ -210,15 +216,27 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     const int sl = i * NT + tid, row = sl / KSPR, col = sl % KSPR;
     kgo[i] = col < a.dch ? (row * (int)a.kss + col * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
-  // V rows are unpadded, chunk c of row r at slot c ^ vswz(r); the rows of one
-  // instruction's slots differ from the next's by NT / KCH (a multiple of 4),
-  // so every instruction shares the lane's chunk and only the row base moves
-  constexpr int VI = BN * KCH / NT;
-  static_assert(BN * KCH % NT == 0 && (NT / KCH) % 4 == 0, "V staging covers whole rows");
-  int vgo;
-  {
+  // V rows are unpadded, chunk c of row r at slot c ^ vswz(r). Where a row
+  // has a power-of-two count of chunks, the rows of one instruction's slots
+  // differ from the next's by NT / KCH (a multiple of 4), so every instruction
+  // shares the lane's chunk and only the row base moves; 96-dim rows (12
+  // chunks, no swizzle) take an offset per instruction, the last one covering
+  // the tile's remaining 128 slots.
+  constexpr bool VWHOLE = NT % KCH == 0;
+  constexpr int VSLOTS = BN * KCH;
+  constexpr int VI = (VSLOTS + NT - 1) / NT;
+  static_assert(VWHOLE ? (VSLOTS % NT == 0 && (NT / KCH) % 4 == 0) : (D == 96 && VSLOTS % 64 == 0),
+                "V staging covers whole rows, or whole waves of slots");
+  int vgo[VWHOLE ? 1 : VI];
+  if constexpr (VWHOLE) {
     const int row = tid / KCH, pos = tid % KCH, chunk = pos ^ vswz<D>(row);
-    vgo = chunk < a.dch ? (row * (int)a.vss + chunk * 8) * (int)sizeof(T) : (int)kPadOffset;
+    vgo[0] = chunk < a.dch ? (row * (int)a.vss + chunk * 8) * (int)sizeof(T) : (int)kPadOffset;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int sl = i * NT + tid, row = sl / KCH, chunk = sl % KCH;
+      vgo[i] = chunk < a.dch ? (row * (int)a.vss + chunk * 8) * (int)sizeof(T) : (int)kPadOffset;
+    }
   }
   // this lane's element offsets: K fragment kk at k_lane + 16 kk (row r32,
   // dims 16kk + 8g ..), and the transposing V reads (see pv)
@@ -246,8 +264,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   auto dma_v = [&](int t, int buf) {
     const int tile = t * BN * (int)a.vss * (int)sizeof(T);
 #pragma unroll
-    for (int i = 0; i < VI; ++i)
-      ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo, tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
+    for (int i = 0; i < VI; ++i) {
+      if constexpr (VWHOLE)
+        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[0],
+                   tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
+      else if (VSLOTS % NT == 0 || i * NT + wave * 64 < VSLOTS)  // wave-uniform
+        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
+    }
   };
   auto landed = [&]() { lds_loads_landed(); };
   // S^T of the K tile in buffer buf
@@ -515,15 +538,19 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   a.dch = (int)(head_dim / 8);
   if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 64, 128 or 256 dims, the chunks past head_dim reading as zeros
+  // rows are laid out at 64, 96 (16-bit types), 128 or 256 dims, the chunks past head_dim reading as zeros
   if (dtype == PK_F32)
     return head_dim <= 64 ? launch_f32<64>(a, causal, s)
                           : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (dtype == PK_BF16)
-    return head_dim <= 64 ? launch<bf16, 64>(a, causal, s)
-                          : head_dim <= 128 ? launch<bf16, 128>(a, causal, s) : launch<bf16, 256>(a, causal, s);
-  return head_dim <= 64 ? launch<f16, 64>(a, causal, s)
-                        : head_dim <= 128 ? launch<f16, 128>(a, causal, s) : launch<f16, 256>(a, causal, s);
+    return head_dim <= 64    ? launch<bf16, 64>(a, causal, s)
+           : head_dim <= 96  ? launch<bf16, 96>(a, causal, s)
+           : head_dim <= 128 ? launch<bf16, 128>(a, causal, s)
+                             : launch<bf16, 256>(a, causal, s);
+  return head_dim <= 64    ? launch<f16, 64>(a, causal, s)
+         : head_dim <= 96  ? launch<f16, 96>(a, causal, s)
+         : head_dim <= 128 ? launch<f16, 128>(a, causal, s)
+                           : launch<f16, 256>(a, causal, s);
 }
 
 }  // namespace
