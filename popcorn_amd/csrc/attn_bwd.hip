@@ -114,7 +114,9 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 template <int D> struct Tile {
   static constexpr int ST = D;
   static __device__ __forceinline__ int swz(int row) {
-    if constexpr (D >= 128)
+    if constexpr (D == 96)  // 12 chunks: rows start 0, 192, 128, 64 bytes into a bank window, period 4
+      return (row >> 2) & 3;
+    else if constexpr (D >= 128)
       return 4 * (row & 3) + ((row >> 2) & 3);
     else
       return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
@@ -145,12 +147,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
   constexpr int KCH = D / 8;
-  constexpr int TI = BN * KCH / NT;  // direct loads per thread per tile of K (and of V): 4, 2 or 1
+  constexpr int TSLOTS = BN * KCH;   // 16-byte slots of a K (or V) tile
+  constexpr int TI = (TSLOTS + NT - 1) / NT;  // direct loads per thread per tile of K (and of V): 4, 2 or 1
+  // 96-dim rows: a tile is 384 slots, and the second load of waves 2 and 3
+  // lies past it; they load nothing (out of range) into `spill`, so every wave
+  // issues the same loads and its vmcnt counts hold
+  constexpr bool TFULL = TSLOTS % NT == 0;
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   constexpr int NSQ = 4;  // K/V tile stages: the two tiles a step reads, one in flight, one landing
   __shared__ __attribute__((aligned(16))) T Ks[NSQ][BN * L::ST];
   __shared__ __attribute__((aligned(16))) T Vs[NSQ][BN * L::ST];
+  __shared__ __attribute__((aligned(16))) T spill[TFULL ? 8 : 64 * 8];
 
   // work item: (q tile, batch, kv head, head quad), longest causal rows
   // first; the waves are gp q heads of one kv group (gp = 4, 2 or 1, the
@@ -235,14 +243,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
     const int sl = i * NT + tid, row = sl / KCH, c = (sl % KCH) ^ L::swz(row);
-    kgo[i] = c < a.dch ? (row * (int)a.ks[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
-    vgo[i] = c < a.dch ? (row * (int)a.vs[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
+    const bool in = c < a.dch && sl < TSLOTS;
+    kgo[i] = in ? (row * (int)a.ks[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
+    vgo[i] = in ? (row * (int)a.vs[1] + c * 8) * (int)sizeof(T) : (int)kPadOffset;
   }
   auto issue = [&](int t, int buf) {
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
-      ld_buf_lds(krsrc, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(T));
-      ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(T));
+      const bool in = TFULL || i * NT + wave * 64 < TSLOTS;  // wave-uniform
+      ld_buf_lds(krsrc, in ? Ks[buf] + (i * NT + wave * 64) * 8 : spill, kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(T));
+      ld_buf_lds(vrsrc, in ? Vs[buf] + (i * NT + wave * 64) * 8 : spill, vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(T));
     }
   };
   // lane offsets: K / V fragment kk (A operand: row r32, dims 16kk + 8g) and the
@@ -405,7 +415,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   using L = Tile<D>;
   constexpr int KCH = D / 8;             // 16-byte chunks per row
   constexpr int SLOTS = BQ * KCH;        // 16-byte slots of a Q (or dO) tile: 512 or 256
-  constexpr int TI = 2 * SLOTS / NT2;    // direct loads per thread per tile (Q and dO together): 2 or 1
+  constexpr int TI = (2 * SLOTS + NT2 - 1) / NT2;  // direct loads per thread per tile (Q and dO together): 2 or 1
+  // 96-dim rows: a stage is 768 slots, and the second load of waves 4-7 lies
+  // past it; they load nothing (out of range) into `tspill`, so every wave
+  // issues the same loads and its vmcnt counts hold
+  constexpr bool TFULL = 2 * SLOTS % NT2 == 0;
   constexpr int NS = 6;                  // query tiles resident or in flight in LDS
   constexpr int PER_ISSUE = TI + 1;      // loads each wave issues per tile (tiles, one row vector)
   constexpr int TILE = BQ * D;
@@ -415,6 +429,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   __shared__ __attribute__((aligned(16))) T QG[NS][2 * TILE];
   __shared__ __attribute__((aligned(16))) float RV[NS][2][64];
   __shared__ __attribute__((aligned(16))) float spill[64];
+  __shared__ __attribute__((aligned(16))) T tspill[TFULL ? 8 : 64 * 8];
   // P of each key slice as fp16 (P <= 1; 11 significant bits, more than the
   // rounded dS it feeds), double-buffered: [buffer][slice][16 values x 64 lanes]
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -481,7 +496,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   for (int i = 0; i < TI; ++i) {
     const int sl = i * NT2 + tid, op = sl / SLOTS, within = sl % SLOTS;
     const int row = within / KCH, c = (within % KCH) ^ L::swz(row);
-    go[i] = c < a.dch ? (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T) : (int)kPadOffset;
+    go[i] = c < a.dch && op < 2 ? (row * (int)(op == 0 ? a.qs[1] : a.gs[1]) + c * 8) * (int)sizeof(T)
+                                : (int)kPadOffset;
   }
   // Tiles are issued in order: a cursor holds the next tile's q head (within
   // the group) and q tile, and the buffer descriptors of that head, rebuilt
@@ -512,7 +528,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   auto issue = [&](int st) {
     const int r0 = (u0 + cur_u) * BQ;
 #pragma unroll
-    for (int i = 0; i < TI; ++i) ld_buf_lds(trs[i], QG[st] + (i * NT2 + wave * 64) * 8, go[i], r0 * tstride[i]);
+    for (int i = 0; i < TI; ++i) {
+      const bool in = TFULL || i * NT2 + wave * 64 < 2 * SLOTS;  // wave-uniform
+      ld_buf_lds(trs[i], in ? QG[st] + (i * NT2 + wave * 64) * 8 : tspill, go[i], r0 * tstride[i]);
+    }
     ld_buf_lds4(rrs, wave == 0 ? RV[st][0] : (wave == 1 ? RV[st][1] : spill), lane * (int)sizeof(float),
                 r0 * (int)sizeof(float));
     if (cur_it + 1 < n_it) {
@@ -805,7 +824,8 @@ inline int64_t round_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; 
 
 // Workspace bytes: D and lse2 (2 * lse_n floats), then the dk/dv partials when
 // the kernel splits the q heads.
-// (The partials are laid out at the kernels' row width: 64, 128 or 256 dims.)
+// (The partials are laid out at the kernels' row width: 64, 96, 128 or 256 dims; fp32, whose
+// kernels have no 96-dim layout, is counted at 128, which covers either.)
 int64_t workspace_bytes(int64_t lse_n, int64_t rows, int64_t kv_heads, int64_t head_dim, int nsplit) {
   const int64_t width = head_dim <= 64 ? 64 : (head_dim <= 128 ? 128 : 256);
   const int64_t parts = nsplit > 1 ? (int64_t)nsplit * 2 * rows * kv_heads * width * (int64_t)sizeof(float) : 0;
@@ -869,13 +889,18 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.dch = (int)(head_dim / 8);
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 64 or 128 dims, the chunks past head_dim reading as zeros
+  // rows are laid out at 64, 96 (16-bit types), 128 or 256 dims, the chunks past head_dim reading as zeros
   if (dtype == PK_F32)
     return head_dim <= 64 ? launch_f32<64>(a, causal, s)
                           : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (head_dim > 128) return dtype == PK_BF16 ? launch_wide<bf16>(a, causal, s) : launch_wide<f16>(a, causal, s);
-  if (dtype == PK_BF16) return head_dim <= 64 ? launch<bf16, 64>(a, causal, s) : launch<bf16, 128>(a, causal, s);
-  return head_dim <= 64 ? launch<f16, 64>(a, causal, s) : launch<f16, 128>(a, causal, s);
+  if (dtype == PK_BF16)
+    return head_dim <= 64   ? launch<bf16, 64>(a, causal, s)
+           : head_dim <= 96 ? launch<bf16, 96>(a, causal, s)
+                            : launch<bf16, 128>(a, causal, s);
+  return head_dim <= 64 ? launch<f16, 64>(a, causal, s)
+         : head_dim <= 96 ? launch<f16, 96>(a, causal, s)
+                          : launch<f16, 128>(a, causal, s);
 }
 
 }  // namespace

@@ -1,12 +1,12 @@
 """Attention at every head_dim of Popcorn's grid (core/dims.py:74), forward and backward, on the GPU.
 
-The kernels lay rows out at 64, 96 and 192 (16-bit forward), 128 or 256 dims and read
-zeros past the tensors' head_dim, so any multiple of 8 up to 256 is served
-forward and backward. Each case is graded against the float64 oracle with
-Popcorn's pass rule (budget: the registered reference at native dtype, on the
-CPU), and the layouts are checked against each other directly: a head_dim-96
-call (the 96-dim forward layout, the 128-dim backward one) gives the same bits
-as the head_dim-128 kernels on the same rows zero-padded to 128.
+The kernels lay rows out at 64, 96 (16-bit), 128, 192 (16-bit forward) or 256
+dims and read zeros past the tensors' head_dim, so any multiple of 8 up to 256
+is served forward and backward. Each case is graded against the float64 oracle
+with Popcorn's pass rule (budget: the registered reference at native dtype, on
+the CPU), and the layouts are checked against each other directly: a
+head_dim-96 call (the 96-dim layouts) gives the same bits as the head_dim-128
+kernels on the same rows zero-padded to 128.
 """
 
 import numpy as np
@@ -72,7 +72,7 @@ def test_attn_backward_head_dims(seq, hq, hkv, causal, d, dtype):
 def test_attn_head_dim_96_is_the_128_kernel_on_zero_padded_rows():
     """Forward and backward bits of head_dim 96 equal those of head_dim 128 on inputs zero-padded
     to 128 (with the 96-dim scale), and the padded dims of the 128 call's gradients are zero: the
-    96-dim forward layout skips only products of zeros."""
+    96-dim layouts skip only products of zeros."""
     b, s, hq, hkv, d = 2, 190, 8, 2, 96
     q, k, v = (t.to(DEV) for t in _qkv(b, s, hq, hkv, d, torch.bfloat16, seed=21))
     do = seeded((b, s, hq, d), 25, torch.bfloat16).to(DEV)
