@@ -80,7 +80,7 @@ constexpr int BN = 32;
 constexpr int NT = 256;
 // fragment reads in flight ahead of the product that uses them (head_dim 256,
 // whose Q^T fragments and O^T accumulators take 192 registers, keeps fewer)
-template <int D> constexpr int kRing = D >= 192 ? 3 : 6;
+template <int D> constexpr int kRing = D >= 192 ? 3 : (D == 32 ? 4 : 6);  // at most the step's 2 * D / 16 products
 // Buffer offset of a padding slot: at or past every range the kernel builds
 // (each below 2^31), and with a tile offset below 2^31 added it cannot wrap.
 constexpr uint32_t kPadOffset = 0x80000000u;
@@ -91,7 +91,7 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 // 96-dim rows, 192 bytes, already start 64 bytes apart modulo the window, and
 // 192-dim rows, 384 bytes, 128 bytes apart, which the swizzle halves).
 template <int D> __device__ __forceinline__ int vswz(int r) {
-  if constexpr (D == 96) return 0;
+  if constexpr (D == 32 || D == 96) return 0;  // 64-byte rows: four of them fill the window
   else if constexpr (D == 192) return 4 * ((r >> 1) & 1);
   else return D >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
 }
@@ -221,13 +221,13 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // V rows are unpadded, chunk c of row r at slot c ^ vswz(r). Where a row
   // has a power-of-two count of chunks, the rows of one instruction's slots
   // differ from the next's by NT / KCH (a multiple of 4), so every instruction
-  // shares the lane's chunk and only the row base moves; 96- and 192-dim rows
-  // (12 and 24 chunks) take an offset per instruction (for 96 dims the last
-  // one covers the tile's remaining 128 slots).
-  constexpr bool VWHOLE = NT % KCH == 0;
+  // shares the lane's chunk and only the row base moves; 32-, 96- and 192-dim
+  // rows (4, 12 and 24 chunks) take an offset per instruction (for 32 and 96
+  // dims the last one covers the tile's remaining 128 slots).
   constexpr int VSLOTS = BN * KCH;
+  constexpr bool VWHOLE = NT % KCH == 0 && VSLOTS % NT == 0;
   constexpr int VI = (VSLOTS + NT - 1) / NT;
-  static_assert(VWHOLE ? (VSLOTS % NT == 0 && (NT / KCH) % 4 == 0) : ((D == 96 || D == 192) && VSLOTS % 64 == 0),
+  static_assert(VWHOLE ? (NT / KCH) % 4 == 0 : ((D == 32 || D == 96 || D == 192) && VSLOTS % 64 == 0),
                 "V staging covers whole rows, or whole waves of slots");
   int vgo[VWHOLE ? 1 : VI];
   if constexpr (VWHOLE) {
@@ -540,18 +540,20 @@ int attn_launch(const char* who, AttnArgs a, const int64_t* strides, int64_t bat
   a.dch = (int)(head_dim / 8);
   if ((int64_t)a.m_tiles * batch * q_heads / a.gp > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 64, 96 (16-bit types), 128, 192 (16-bit types) or 256 dims, the chunks past
+  // rows are laid out at 32, 96 and 192 (16-bit types), 64, 128 or 256 dims, the chunks past
   // head_dim reading as zeros
   if (dtype == PK_F32)
     return head_dim <= 64 ? launch_f32<64>(a, causal, s)
                           : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (dtype == PK_BF16)
-    return head_dim <= 64    ? launch<bf16, 64>(a, causal, s)
+    return head_dim <= 32    ? launch<bf16, 32>(a, causal, s)
+           : head_dim <= 64  ? launch<bf16, 64>(a, causal, s)
            : head_dim <= 96  ? launch<bf16, 96>(a, causal, s)
            : head_dim <= 128 ? launch<bf16, 128>(a, causal, s)
            : head_dim <= 192 ? launch<bf16, 192>(a, causal, s)
                              : launch<bf16, 256>(a, causal, s);
-  return head_dim <= 64    ? launch<f16, 64>(a, causal, s)
+  return head_dim <= 32    ? launch<f16, 32>(a, causal, s)
+         : head_dim <= 64  ? launch<f16, 64>(a, causal, s)
          : head_dim <= 96  ? launch<f16, 96>(a, causal, s)
          : head_dim <= 128 ? launch<f16, 128>(a, causal, s)
          : head_dim <= 192 ? launch<f16, 192>(a, causal, s)
