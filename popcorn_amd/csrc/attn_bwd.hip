@@ -75,7 +75,7 @@ constexpr int BN = 32;   // dq kernel: keys per tile
 constexpr int BK = 128;  // dkdv kernel: keys per block
 constexpr int BQ = 32;   // dkdv kernel: query rows per tile
 constexpr int kRingDq = 3;    // dq kernel: fragment reads in flight ahead of their product
-constexpr int kRingDkdv = 5;  // dkdv kernel: the same
+template <int D> constexpr int kRingDkdv = D == 32 ? 4 : 5;  // dkdv kernel: the same (at most a step's products)
 
 struct BwdArgs {
   const void *q, *k, *v, *o, *dout;
@@ -114,7 +114,7 @@ constexpr uint32_t kPadOffset = 0x80000000u;
 template <int D> struct Tile {
   static constexpr int ST = D;
   static __device__ __forceinline__ int swz(int row) {
-    if constexpr (D == 96)  // 12 chunks: rows start 0, 192, 128, 64 bytes into a bank window, period 4
+    if constexpr (D == 32 || D == 96)  // 4 or 12 chunks: rows start 64 bytes apart in a bank window, period 4
       return (row >> 2) & 3;
     else if constexpr (D >= 128)
       return 4 * (row & 3) + ((row >> 2) & 3);
@@ -407,9 +407,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 constexpr int NT2 = 512;  // dkdv kernel: 8 waves, two per SIMD
 
-// head_dim 64 fits 128 registers, so two blocks share a CU (four waves per SIMD)
+// head_dim 32 and 64 fit 128 registers, so two blocks (or more) share a CU (four waves per SIMD)
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void attn_bwd_dkdv_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(D <= 64 ? 4 : 2))) void attn_bwd_dkdv_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
@@ -600,7 +600,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   // reads of the tile at abase: 16 keys c = h / DT, dims 32 (h % DT) ..; B =
   // mf[c]), product 2h + 1 is score step h (A from the tile at pbase, B = the
   // lane's key row) into sres. Fragment reads run kRingDkdv products ahead.
-  constexpr int RING = kRingDkdv;
+  constexpr int RING = kRingDkdv<D>;
   constexpr int NP = 2 * KK;
   static_assert(RING <= NP, "the ring's first reads stay inside the run");
   f32x16 sres;  // score block of the wave's next tile
@@ -889,16 +889,18 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.dch = (int)(head_dim / 8);
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 64, 96 (16-bit types), 128 or 256 dims, the chunks past head_dim reading as zeros
+  // rows are laid out at 32 and 96 (16-bit types), 64, 128 or 256 dims, the chunks past head_dim reading as zeros
   if (dtype == PK_F32)
     return head_dim <= 64 ? launch_f32<64>(a, causal, s)
                           : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
   if (head_dim > 128) return dtype == PK_BF16 ? launch_wide<bf16>(a, causal, s) : launch_wide<f16>(a, causal, s);
   if (dtype == PK_BF16)
-    return head_dim <= 64   ? launch<bf16, 64>(a, causal, s)
+    return head_dim <= 32   ? launch<bf16, 32>(a, causal, s)
+           : head_dim <= 64 ? launch<bf16, 64>(a, causal, s)
            : head_dim <= 96 ? launch<bf16, 96>(a, causal, s)
                             : launch<bf16, 128>(a, causal, s);
-  return head_dim <= 64 ? launch<f16, 64>(a, causal, s)
+  return head_dim <= 32   ? launch<f16, 32>(a, causal, s)
+         : head_dim <= 64 ? launch<f16, 64>(a, causal, s)
          : head_dim <= 96 ? launch<f16, 96>(a, causal, s)
                           : launch<f16, 128>(a, causal, s);
 }
