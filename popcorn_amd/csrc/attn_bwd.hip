@@ -116,6 +116,8 @@ template <int D> struct Tile {
   static __device__ __forceinline__ int swz(int row) {
     if constexpr (D == 32 || D == 96)  // 4 or 12 chunks: rows start 64 bytes apart in a bank window, period 4
       return (row >> 2) & 3;
+    else if constexpr (D == 192)  // 24 chunks: rows start 128 bytes apart; the swizzle stays in groups of 8 chunks
+      return (4 * ((row >> 1) & 1)) | ((row >> 2) & 1) | (2 * ((row >> 3) & 1));
     else if constexpr (D >= 128)
       return 4 * (row & 3) + ((row >> 2) & 3);
     else
@@ -140,9 +142,9 @@ __device__ __forceinline__ uint4 flip(uint4 v, uint32_t f) { return make_uint4(v
 
 // ------------------------------------------------------------------ dq kernel
 
-// head_dim 256 holds Q, dO and the dQ accumulator in 256 registers: one wave per SIMD
+// head_dim 192 and 256 hold Q, dO and the dQ accumulator in 192 or 256 registers: one wave per SIMD
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void attn_bwd_dq_kernel(
+__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(D >= 192 ? 1 : 2))) void attn_bwd_dq_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
@@ -889,11 +891,15 @@ int bwd_launch(const char* who, BwdArgs a, void* workspace, int64_t workspace_by
   a.dch = (int)(head_dim / 8);
   if ((seq + BM - 1) / BM * batch * q_heads > INT32_MAX) return fail(PK_ERR_UNSUPPORTED, "%s: grid too large", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // rows are laid out at 32 and 96 (16-bit types), 64, 128 or 256 dims, the chunks past head_dim reading as zeros
+  // rows are laid out at 32, 96 and 192 (16-bit types), 64, 128 or 256 dims, the chunks past head_dim reading
+  // as zeros
   if (dtype == PK_F32)
     return head_dim <= 64 ? launch_f32<64>(a, causal, s)
                           : (head_dim <= 128 ? launch_f32<128>(a, causal, s) : launch_f32<256>(a, causal, s));
-  if (head_dim > 128) return dtype == PK_BF16 ? launch_wide<bf16>(a, causal, s) : launch_wide<f16>(a, causal, s);
+  if (head_dim > 192)
+    return dtype == PK_BF16 ? launch_wide<bf16, 256>(a, causal, s) : launch_wide<f16, 256>(a, causal, s);
+  if (head_dim > 128)
+    return dtype == PK_BF16 ? launch_wide<bf16, 192>(a, causal, s) : launch_wide<f16, 192>(a, causal, s);
   if (dtype == PK_BF16)
     return head_dim <= 32   ? launch<bf16, 32>(a, causal, s)
            : head_dim <= 64 ? launch<bf16, 64>(a, causal, s)

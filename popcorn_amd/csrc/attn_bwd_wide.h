@@ -1,5 +1,5 @@
-// Attention dK/dV at head_dim 256 (and 136-248, laid out at 256) for the
-// 16-bit dtypes. Included by attn_bwd.hip inside its namespace, after
+// Attention dK/dV at head_dim 192 and 256 (136-184 laid out at 192, 200-248
+// at 256) for the 16-bit dtypes. Included by attn_bwd.hip inside its namespace, after
 // dkdv_sum_kernel. The work mapping (128 keys of one (sequence, kv head) per
 // block, q-head splits with fp32 partials), the workspace, the LDS swizzle and
 // the fragment layouts are the head_dim 64/128 dk/dv kernel's; what changes is
@@ -20,7 +20,7 @@ constexpr int kWideThreads = 256;  // four 32-key slices, one wave each
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWideThreads, kWideThreads), amdgpu_waves_per_eu(1)))
 void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
-  static_assert(D == 128 || D == 256, "rows of 128 or 256 dims");
+  static_assert(D == 128 || D == 192 || D == 256, "rows of 128, 192 or 256 dims");
   using Frag = typename Mma<T>::frag;
   using L = Tile<D>;
   constexpr int KCH = D / 8;                    // 16-byte chunks per row
@@ -111,11 +111,12 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
     }
   };
 
-  // Lane offsets of the fragment reads. At 256 dims chunks 16 .. 31 of a row
-  // keep their swizzle 16 chunks on, so the second half of the row (h >= 8,
-  // dt >= 4) is the first half's offset plus 128 elements.
-  constexpr int HALVES = D / 128;
-  constexpr int KH = KK / HALVES, DH = DT / HALVES;
+  // Lane offsets of the fragment reads. The tile swizzle repeats every PERIOD
+  // elements of a row (128 at 128 and 256 dims, 64 at 192), so fragment h
+  // (or block dt) of a later period is the first period's offset plus whole
+  // periods.
+  constexpr int PERIOD = D == 192 ? 64 : 128;
+  constexpr int KH = PERIOD / 16, DH = PERIOD / 32;
   int a_lane[KH], t_lane[2][DH];
 #pragma unroll
   for (int h = 0; h < KH; ++h) a_lane[h] = L::at(r32, 16 * h + 8 * g);
@@ -126,11 +127,11 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
       t_lane[hi][dt] = L::at(8 * hi + 4 * g + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
   // row fragment h of a tile (A operand of a score product: its 32 rows, dims 16 h + 8 g ..)
   auto row_frag = [&](const T* tile, int h) -> Frag {
-    return *reinterpret_cast<const Frag*>(tile + a_lane[h % KH] + (h / KH) * 128);
+    return *reinterpret_cast<const Frag*>(tile + a_lane[h % KH] + (h / KH) * PERIOD);
   };
   // transposed fragment of a tile (A operand of an accumulation: dims 32 dt + row l % 32, rows of chunk c)
   auto col_frag = [&](const T* tile, int c, int dt) -> Frag {
-    const int off = 16 * c * L::ST + (dt / DH) * 128;
+    const int off = 16 * c * L::ST + (dt / DH) * PERIOD;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[0][dt % DH] + off));
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + t_lane[1][dt % DH] + off));
     return __builtin_bit_cast(Frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -259,21 +260,21 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
   }
 }
 
-// head_dim 136-256 in bf16 or fp16: the dq kernel at 256 dims and the single-role dk/dv kernel
-template <typename T> int launch_wide(const BwdArgs& a, bool causal, hipStream_t s) {
+// head_dim 136-256 in bf16 or fp16 (rows of D = 192 or 256): the dq kernel at D and the single-role dk/dv kernel
+template <typename T, int D> int launch_wide(const BwdArgs& a, bool causal, hipStream_t s) {
   const int gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
   const int64_t dq_blocks = (int64_t)((a.S + 32 * (4 / gp) - 1) / (32 * (4 / gp))) * a.B * a.Hq / gp;
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv * a.nsplit;
   if (causal) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, 256, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, 256, true>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, D, true>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, 256, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, 256, false>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_wide_kernel<T, D, false>), dim3(kv_blocks), dim3(kWideThreads), 0, s, a);
   }
   if (a.nsplit > 1) {
     const int64_t n = a.rows * a.Hkv * (a.dr / 4);
-    hipLaunchKernelGGL((dkdv_sum_kernel<T, 256>), dim3((n + 255) / 256), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dkdv_sum_kernel<T, D>), dim3((n + 255) / 256), dim3(256), 0, s, a);
   }
   return launched("pk_attn_bwd");
 }

@@ -1,7 +1,7 @@
 """Attention at every head_dim of Popcorn's grid (core/dims.py:74), forward and backward, on the GPU.
 
-The kernels lay rows out at 32 and 96 (16-bit), 64, 128, 192 (16-bit forward)
-or 256 dims and read zeros past the tensors' head_dim, so any multiple of 8 up to 256
+The kernels lay rows out at 32, 96 and 192 (16-bit), 64, 128 or 256 dims and
+read zeros past the tensors' head_dim, so any multiple of 8 up to 256
 is served forward and backward. Each case is graded against the float64 oracle
 with Popcorn's pass rule (budget: the registered reference at native dtype, on
 the CPU), and the layouts are checked against each other directly: a
