@@ -256,7 +256,8 @@ def test_attn_varlen_bwd_dkdv_direct_and_partial_splits(seqs, length, splits):
 
 
 # --------------------------------------------------------------------------- head_dim 136-256
-# Rows past 128 dims take the dq kernel at 256 and the single-role dk/dv kernel.
+# Rows past 128 dims take the wide path (a dq kernel and the single-role dk/dv
+# kernel): 16-bit head_dim 136-192 is laid out at 192 dims, 200-256 at 256.
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
@@ -267,9 +268,9 @@ def test_attn_bwd_wide_head_dims(seq, causal, d, dtype):
     _check(2, seq, 8, 2, d, causal, None, dtype)
 
 
-@pytest.mark.parametrize("d", [136, 160, 248])
-def test_attn_bwd_wide_head_dims_laid_out_at_256(d):
-    """head_dim between 128 and 256: the dims past it read as zeros and are never stored."""
+@pytest.mark.parametrize("d", [136, 160, 184, 200, 248])
+def test_attn_bwd_wide_head_dims_padded_layouts(d):
+    """head_dim inside the 192- or 256-dim layout: the dims past it read as zeros and are never stored."""
     _check(1, 77, 4, 1, d, True, None, torch.bfloat16, seed=4)
 
 
