@@ -142,8 +142,11 @@ __device__ __forceinline__ uint4 flip(uint4 v, uint32_t f) { return make_uint4(v
 
 // ------------------------------------------------------------------ dq kernel
 
-// head_dim 192 and 256 hold Q, dO and the dQ accumulator in 192 or 256 registers: one wave per SIMD
-template <typename T, int D, bool CAUSAL>
+// head_dim 192 and 256 hold Q, dO and the dQ accumulator in 192 or 256 registers: one wave per SIMD.
+// KS: 16-dim steps of the S and dP products, D / 16, or one fewer when the
+// row's last 16 dims are all past head_dim (zeros in every operand of that
+// step, so skipping it changes no bit)
+template <typename T, int D, bool CAUSAL, int KS = D / 16>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(D >= 192 ? 1 : 2))) void attn_bwd_dq_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
@@ -158,6 +161,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
   constexpr int NSQ = 4;  // K/V tile stages: the two tiles a step reads, one in flight, one landing
+  static_assert(KS == KK || KS == KK - 1, "at most the last 16-dim step is skipped");
   __shared__ __attribute__((aligned(16))) T Ks[NSQ][BN * L::ST];
   __shared__ __attribute__((aligned(16))) T Vs[NSQ][BN * L::ST];
   __shared__ __attribute__((aligned(16))) T spill[TFULL ? 8 : 64 * 8];
@@ -288,16 +292,20 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   // product 3h: dQ step h (A = K^T from transposing reads of the tile at ka:
   // 16 keys c = h / DT, dims 32 (h % DT) ..; B = dsf[c]); 3h + 1: S^T step h
   // (A = K fragment h of the tile at kn, B = Q^T); 3h + 2: dP^T step h (A = V
-  // fragment h of the tile at vn, B = dO^T). Reads run kRingDq products ahead.
+  // fragment h of the tile at vn, B = dO^T). With KS < KK the run ends with
+  // the last dQ step alone. Reads run kRingDq products ahead.
   constexpr int RING = kRingDq;
-  constexpr int NP = 3 * KK;
+  constexpr int NP = KK + 2 * KS;
   static_assert(RING <= NP, "the ring's first reads stay inside the run");
+  // product i: its kind (0 dQ, 1 S^T, 2 dP^T) and step h
+  auto kind = [](int i) { return i < 3 * KS ? i % 3 : 0; };
+  auto step_of = [](int i) { return i < 3 * KS ? i / 3 : KS + (i - 3 * KS); };
   f32x16 s, dp;  // S^T and dP^T of the wave's next tile
   auto run = [&](const T* ka, const Frag (&dsf)[2], const T* kn, const T* vn) {
     auto fetch = [&](int i) -> Frag {
-      const int h = i / 3;
-      if (i % 3 == 1) return *reinterpret_cast<const Frag*>(kn + a_lane[h]);
-      if (i % 3 == 2) return *reinterpret_cast<const Frag*>(vn + a_lane[h]);
+      const int h = step_of(i);
+      if (kind(i) == 1) return *reinterpret_cast<const Frag*>(kn + a_lane[h]);
+      if (kind(i) == 2) return *reinterpret_cast<const Frag*>(vn + a_lane[h]);
       const int c = h / DT, dt = h % DT;
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ka + t_lane[0][dt] + 16 * c * L::ST));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(ka + t_lane[1][dt] + 16 * c * L::ST));
@@ -312,10 +320,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     for (int i = 0; i < NP; ++i) {
       const Frag f = ring[i % RING];
       if (i + RING < NP) ring[i % RING] = fetch(i + RING);
-      const int h = i / 3;
-      if (i % 3 == 0)
+      const int h = step_of(i);
+      if (kind(i) == 0)
         acc[h % DT] = Mma<T>::run(f, dsf[h / DT], acc[h % DT]);
-      else if (i % 3 == 1)
+      else if (kind(i) == 1)
         s = Mma<T>::run(f, qf[h], s);
       else
         dp = Mma<T>::run(f, gf[h], dp);
@@ -409,8 +417,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 
 constexpr int NT2 = 512;  // dkdv kernel: 8 waves, two per SIMD
 
-// head_dim 32 and 64 fit 128 registers, so two blocks (or more) share a CU (four waves per SIMD)
-template <typename T, int D, bool CAUSAL>
+// head_dim 32 and 64 fit 128 registers, so two blocks (or more) share a CU (four waves per SIMD).
+// KS: 16-dim steps of the score products (S, dP), as in the dq kernel
+template <typename T, int D, bool CAUSAL, int KS = D / 16>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_per_eu(D <= 64 ? 4 : 2))) void attn_bwd_dkdv_kernel(
     BwdArgs a) {
   using Frag = typename Mma<T>::frag;
@@ -427,6 +436,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   constexpr int TILE = BQ * D;
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
+  static_assert(KS == KK || KS == KK - 1, "at most the last 16-dim step is skipped");
   // stage: Q tile then dO tile; row vectors: lse2, then D (64 slots: whole-wave loads)
   __shared__ __attribute__((aligned(16))) T QG[NS][2 * TILE];
   __shared__ __attribute__((aligned(16))) float RV[NS][2][64];
@@ -601,15 +611,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
   // The step's products: product 2h is accumulation h (A^T from transposing
   // reads of the tile at abase: 16 keys c = h / DT, dims 32 (h % DT) ..; B =
   // mf[c]), product 2h + 1 is score step h (A from the tile at pbase, B = the
-  // lane's key row) into sres. Fragment reads run kRingDkdv products ahead.
-  constexpr int RING = kRingDkdv<D>;
-  constexpr int NP = 2 * KK;
-  static_assert(RING <= NP, "the ring's first reads stay inside the run");
+  // lane's key row) into sres; with KS < KK the run ends with the last
+  // accumulation step alone. Fragment reads run kRingDkdv products ahead.
+  constexpr int NP = KK + KS;
+  constexpr int RING = kRingDkdv<D> < NP ? kRingDkdv<D> : NP;
+  // product i: a score step or not, and its step h
+  auto is_score = [](int i) { return i < 2 * KS && (i & 1); };
+  auto step_of = [](int i) { return i < 2 * KS ? i >> 1 : KS + (i - 2 * KS); };
   f32x16 sres;  // score block of the wave's next tile
   auto run = [&](const T* abase, const Frag (&mf)[2], const T* pbase) {
     auto fetch = [&](int i) -> Frag {
-      const int h = i >> 1;
-      if (i & 1) return *reinterpret_cast<const Frag*>(pbase + a_lane[h]);
+      const int h = step_of(i);
+      if (is_score(i)) return *reinterpret_cast<const Frag*>(pbase + a_lane[h]);
       const int c = h / DT, dt = h % DT;
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[0][dt] + 16 * c * L::ST));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(abase + t_lane[1][dt] + 16 * c * L::ST));
@@ -624,8 +637,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT2, NT2), amdgpu_waves_pe
     for (int i = 0; i < NP; ++i) {
       const Frag f = ring[i % RING];
       if (i + RING < NP) ring[i % RING] = fetch(i + RING);
-      const int h = i >> 1;
-      if (i & 1)
+      const int h = step_of(i);
+      if (is_score(i))
         sres = Mma<T>::run(f, bf[h], sres);
       else
         acc[h % DT] = Mma<T>::run(f, mf[h / DT], acc[h % DT]);
@@ -791,23 +804,34 @@ __global__ __launch_bounds__(256) void dkdv_sum_kernel(BwdArgs a) {
 #include "attn_bwd_f32.h"
 #include "attn_bwd_wide.h"
 
-template <typename T, int D>
-int launch(const BwdArgs& a, bool causal, hipStream_t s) {
+template <typename T, int D, int KS>
+int launch_ks(const BwdArgs& a, bool causal, hipStream_t s) {
   const int gp = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
   const int64_t dq_blocks = (int64_t)((a.S + 32 * (4 / gp) - 1) / (32 * (4 / gp))) * a.B * a.Hq / gp;
   const int64_t kv_blocks = (int64_t)((a.S + BK - 1) / BK) * a.B * a.Hkv * a.nsplit;
   if (causal) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, true>), dim3(kv_blocks), dim3(NT2), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, true, KS>), dim3(dq_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, true, KS>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, false>), dim3(dq_blocks), dim3(NT), 0, s, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false>), dim3(kv_blocks), dim3(NT2), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, D, false, KS>), dim3(dq_blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, D, false, KS>), dim3(kv_blocks), dim3(NT2), 0, s, a);
   }
   if (a.nsplit > 1) {
     const int64_t n = a.rows * a.Hkv * (a.dr / 4);
     hipLaunchKernelGGL((dkdv_sum_kernel<T, D>), dim3((n + 255) / 256), dim3(256), 0, s, a);
   }
   return launched("pk_attn_bwd");
+}
+
+// head_dim 40-48 and 72-80 (Popcorn's 48 and 80) leave the last 16 dims of the
+// 64- and 96-dim rows empty: their S and dP steps are skipped. (At 8-16 on the
+// 32-dim rows the shorter runs measured slower: 2.53 against 2.44 ms at C5's
+// shape, head_dim 16.)
+template <typename T, int D>
+int launch(const BwdArgs& a, bool causal, hipStream_t s) {
+  if constexpr (D == 64 || D == 96)
+    if ((a.dr + 15) / 16 < D / 16) return launch_ks<T, D, D / 16 - 1>(a, causal, s);
+  return launch_ks<T, D, D / 16>(a, causal, s);
 }
 
 // Number of q-head splits of the dk/dv kernel: the smallest divisor of the

@@ -121,7 +121,10 @@ struct AttnArgs {
   int dr, dch;
 };
 
-template <typename T, int D, bool CAUSAL>
+// KS: 16-dim steps of the score products, D / 16, or one fewer when the row's
+// last 16 dims are all past head_dim (zeros in Q and K, so the step adds exact
+// zeros and skipping it changes no bit)
+template <typename T, int D, bool CAUSAL, int KS>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(2))) void attn_fwd_kernel(
     AttnArgs a) {
   using Frag = typename Mma<T>::frag;
@@ -129,6 +132,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   constexpr int KCH = D / 8;   // 16-byte chunks per K/V row
   constexpr int KK = D / 16;
   constexpr int DT = D / 32;
+  static_assert(KS == KK || KS == KK - 1, "at most the last 16-dim step is skipped");
   __shared__ __attribute__((aligned(16))) T Ks[2][BN * KST];
   __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
 
@@ -189,9 +193,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
-  Frag qf[KK];
+  Frag qf[KS];
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
+  for (int kk = 0; kk < KS; ++kk) {
     uint4 raw = make_uint4(0, 0, 0, 0);
     if (q_row < S && 2 * kk + g < a.dch)
       raw = *reinterpret_cast<const uint4*>(qbase + (int64_t)q_row * a.qss + 16 * kk + 8 * g);
@@ -282,7 +286,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) s = Mma<T>::run(*reinterpret_cast<const Frag*>(ks + k_lane + 16 * kk), qf[kk], s);
+    for (int kk = 0; kk < KS; ++kk) s = Mma<T>::run(*reinterpret_cast<const Frag*>(ks + k_lane + 16 * kk), qf[kk], s);
     return s;
   };
   // whether tile t holds keys some row of this wave must not see
@@ -372,14 +376,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
       if (i < KK) return vfrag(Vs[P], i / DT, i % DT);
       return *reinterpret_cast<const Frag*>(ks + 16 * (i - KK));
     };
-    constexpr int N = 2 * KK;  // 2 * DT == KK products of each kind
-    Frag ring[kRing<D>];
+    constexpr int N = KK + KS;  // 2 * DT == KK products of V^T P^T, KS of S^T
+    constexpr int R = kRing<D> < N ? kRing<D> : N;
+    Frag ring[R];
 #pragma unroll
-    for (int i = 0; i < kRing<D>; ++i) ring[i] = fetch(i);
+    for (int i = 0; i < R; ++i) ring[i] = fetch(i);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const Frag f = ring[i % kRing<D>];
-      if (i + kRing<D> < N) ring[i % kRing<D>] = fetch(i + kRing<D>);
+      const Frag f = ring[i % R];
+      if (i + R < N) ring[i % R] = fetch(i + R);
       if (i < KK) {
         acc[i % DT] = Mma<T>::run(f, pf[i / DT], acc[i % DT]);
       } else {
@@ -463,14 +468,23 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   }
 }
 
-template <typename T, int D>
-int launch(const AttnArgs& a, bool causal, hipStream_t s) {
+template <typename T, int D, int KS>
+int launch_ks(const AttnArgs& a, bool causal, hipStream_t s) {
   const int64_t blocks = (int64_t)a.m_tiles * a.B * a.Hq / a.gp;
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true>), dim3(blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, true, KS>), dim3(blocks), dim3(NT), 0, s, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false>), dim3(blocks), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, false, KS>), dim3(blocks), dim3(NT), 0, s, a);
   return launched("pk_attn_fwd");
+}
+
+// head_dim 8-16, 40-48 and 72-80 (Popcorn's 16, 48 and 80) leave the last 16
+// dims of the 32-, 64- and 96-dim rows empty: their score step is skipped
+template <typename T, int D>
+int launch(const AttnArgs& a, bool causal, hipStream_t s) {
+  if constexpr (D <= 96)
+    if ((a.dr + 15) / 16 < D / 16) return launch_ks<T, D, D / 16 - 1>(a, causal, s);
+  return launch_ks<T, D, D / 16>(a, causal, s);
 }
 
 }  // namespace
