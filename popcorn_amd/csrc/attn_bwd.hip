@@ -212,6 +212,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int v_bytes = (int)(((int64_t)(S - 1) * a.vs[1] + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
+  // Rows of 192 and 256 dims (one wave per SIMD) stage their tiles through the
+  // inline-assembly loads, so the step's fragment reads do not first wait for
+  // the step's own prefetch; each step then waits for all of its loads before
+  // its closing barrier. (Measured slower at the narrower rows.)
+  constexpr bool kAsmLoads = D >= 192;
+  const rsrc_words kwords = make_rsrc_words(kbase, k_bytes), vwords = make_rsrc_words(vbase, v_bytes);
 
   // Q^T and dO^T fragments of this lane's row (B operands), and D = rowsum(dO * O)
   Frag qf[KK], gf[KK];
@@ -239,6 +245,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     a.dsum[lidx] = dsum;
     a.dsum[a.lse_n + lidx] = lse2;
   }
+  if constexpr (kAsmLoads) {  // the compiler's own loads complete before the first inline-assembly load
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) asm volatile("" ::"v"(qf[kk]), "v"(gf[kk]));
+    asm volatile("" ::"v"(lse2), "v"(dsum));
+  }
 
   const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
@@ -257,8 +268,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
       const bool in = TFULL || i * NT + wave * 64 < TSLOTS;  // wave-uniform
-      ld_buf_lds(krsrc, in ? Ks[buf] + (i * NT + wave * 64) * 8 : spill, kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(T));
-      ld_buf_lds(vrsrc, in ? Vs[buf] + (i * NT + wave * 64) * 8 : spill, vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(T));
+      T* kl = in ? Ks[buf] + (i * NT + wave * 64) * 8 : spill;
+      T* vl = in ? Vs[buf] + (i * NT + wave * 64) * 8 : spill;
+      const int ko = t * BN * (int)a.ks[1] * (int)sizeof(T), vo = t * BN * (int)a.vs[1] * (int)sizeof(T);
+      if constexpr (kAsmLoads) {
+        ld_lds16_asm(kwords, kl, kgo[i], ko);
+        ld_lds16_asm(vwords, vl, vgo[i], vo);
+      } else {
+        ld_buf_lds(krsrc, kl, kgo[i], ko);
+        ld_buf_lds(vrsrc, vl, vgo[i], vo);
+      }
     }
   };
   // lane offsets: K / V fragment kk (A operand: row r32, dims 16kk + 8g) and the
@@ -364,7 +383,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     }
   };
   auto finish = [&]() {
-    loads_landed_but<(NSQ - 3) * 2 * TI>();
+    if constexpr (kAsmLoads)
+      lds_loads_landed();
+    else
+      loads_landed_but<(NSQ - 3) * 2 * TI>();
     __syncthreads();
   };
   {

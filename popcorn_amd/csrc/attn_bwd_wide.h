@@ -11,7 +11,9 @@
 // registers): per query tile S = Q K^T and dP = dO V^T interleaved, then
 // P = exp2(s c - lse2) and dS = P (dP - D) in registers (no P hand-off through
 // LDS), then dV^T += dO^T P and dK^T += Q^T dS interleaved. Q/dO tiles are
-// double-buffered: the next tile's direct loads fly during the current step.
+// double-buffered: the next tile's direct loads (inline assembly, so that the
+// compiler does not wait for them before reading the other buffer) fly during
+// the current step.
 
 #pragma once
 
@@ -69,6 +71,9 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
       kf[h] = __builtin_bit_cast(Frag, x);
       vf[h] = __builtin_bit_cast(Frag, y);
     }
+    // these loads complete before the first inline-assembly load
+#pragma unroll
+    for (int h = 0; h < KK; ++h) asm volatile("" ::"v"(kf[h]), "v"(vf[h]));
   }
   // Q is staged unflipped: a negative scale signs the exponent's coefficient here and dK's final scale
   const float cs = a.q_flip ? -a.c : a.c;
@@ -95,19 +100,16 @@ void attn_bwd_dkdv_wide_kernel(BwdArgs a) {
     const int r0 = (u0 + it % n_u) * BQ;
     const T* qb = static_cast<const T*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const T* gb = static_cast<const T*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
-    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)qb, (short)0, (int)(((int64_t)(S - 1) * a.qs[1] + a.dr) * (int)sizeof(T)), 0x00020000);
-    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)gb, (short)0, (int)(((int64_t)(S - 1) * a.gs[1] + a.dr) * (int)sizeof(T)), 0x00020000);
+    const rsrc_words qrs = make_rsrc_words(qb, (int)(((int64_t)(S - 1) * a.qs[1] + a.dr) * (int)sizeof(T)));
+    const rsrc_words grs = make_rsrc_words(gb, (int)(((int64_t)(S - 1) * a.gs[1] + a.dr) * (int)sizeof(T)));
 #pragma unroll
     for (int i = 0; i < TI; ++i)
-      ld_buf_lds(i < TI / 2 ? qrs : grs, QG[st] + (i * kWideThreads + wave * 64) * 8, go[i],
+      ld_lds16_asm(i < TI / 2 ? qrs : grs, QG[st] + (i * kWideThreads + wave * 64) * 8, go[i],
                  r0 * (int)(i < TI / 2 ? a.qs[1] : a.gs[1]) * (int)sizeof(T));
     if (wave < 2) {
       const float* rb = a.dsum + b * a.lse_bs + hq * a.lse_hs + start + (wave == 0 ? a.lse_n : 0);
-      const __amdgpu_buffer_rsrc_t rrs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)rb, (short)0, S * (int)sizeof(float), 0x00020000);
-      ld_buf_lds4(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
+      const rsrc_words rrs = make_rsrc_words(rb, S * (int)sizeof(float));
+      ld_lds4_asm(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
     }
   };
 

@@ -49,6 +49,41 @@ __device__ __forceinline__ void ld_buf_lds4(__amdgpu_buffer_rsrc_t r, void* lds,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voffset, soffset, 0, 0);
 }
 
+// A buffer resource as its four words (base, 32-bit range, raw-buffer flags),
+// made wave-uniform, for the inline-assembly loads below.
+typedef unsigned rsrc_words __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ rsrc_words make_rsrc_words(const void* base, int nrec) {
+  const uint64_t p = (uint64_t)base;
+  rsrc_words r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane((uint32_t)nrec);
+  r.w = 0x00020000u;
+  return r;
+}
+
+// ld_buf_lds and ld_buf_lds4 as inline assembly (M0 = the wave's LDS base).
+// The compiler does not see these LDS writes, so it waits for none of them
+// before later LDS reads, which it must do for the builtin whenever it cannot
+// tell the written buffer from the one read (one array indexed by stage). The
+// caller waits (lds_loads_landed) before any barrier after which a wave may
+// read what it wrote. It must also let the compiler finish its own vector
+// loads before issuing these: its waits count loads by number, and loads it
+// does not know of would make them wait for more than they mean to.
+__device__ __forceinline__ uint32_t lds_base(const void* lds) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+}
+__device__ __forceinline__ void ld_lds16_asm(rsrc_words r, const void* lds, int voffset, int soffset) {
+  asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lds_base(lds)), "v"(voffset), "s"(r),
+               "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory");
+}
+__device__ __forceinline__ void ld_lds4_asm(rsrc_words r, const void* lds, int voffset, int soffset) {
+  asm volatile("buffer_load_dword %1, %2, %3 offen lds" ::"{m0}"(lds_base(lds)), "v"(voffset), "s"(r),
+               "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory");
+}
+
 // Wait until this wave's LDS-bound buffer loads have landed.
 __device__ __forceinline__ void lds_loads_landed() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
