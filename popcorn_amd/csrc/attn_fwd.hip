@@ -191,6 +191,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
+  // 192-dim rows stage their tiles through the inline-assembly loads, so the
+  // step's fragment reads do not first wait for the step's own prefetch (each
+  // step waits for all its loads before its closing barrier). Measured slower
+  // at 128 dims, and at 256 the extra registers spill.
+  constexpr bool kAsmLoads = D == 192;
+  const rsrc_words kwords = make_rsrc_words(kbase, k_bytes), vwords = make_rsrc_words(vbase, v_bytes);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
   Frag qf[KS];
@@ -204,6 +210,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     raw.z ^= a.q_flip;
     raw.w ^= a.q_flip;
     qf[kk] = __builtin_bit_cast(Frag, raw);
+  }
+  if constexpr (kAsmLoads) {  // the compiler's own loads complete before the first inline-assembly load
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) asm volatile("" ::"v"(qf[kk]));
   }
 
   const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
@@ -265,17 +275,33 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
 #pragma unroll
     for (int i = 0; i < KI; ++i)
       if (KSLOTS % NT == 0 || i * NT + tid < KSLOTS)
-        ld_buf_lds(krsrc, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], tile);
+      {
+        if constexpr (kAsmLoads)
+          ld_lds16_asm(kwords, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], tile);
+        else
+          ld_buf_lds(krsrc, Ks[buf] + (i * NT + wave * 64) * 8, kgo[i], tile);
+      }
   };
   auto dma_v = [&](int t, int buf) {
     const int tile = t * BN * (int)a.vss * (int)sizeof(T);
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
       if constexpr (VWHOLE)
-        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[0],
-                   tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
+      {
+        if constexpr (kAsmLoads)
+          ld_lds16_asm(vwords, Vs[buf] + (i * NT + wave * 64) * 8, vgo[0],
+                       tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
+        else
+          ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[0],
+                     tile + i * (NT / KCH) * (int)a.vss * (int)sizeof(T));
+      }
       else if (VSLOTS % NT == 0 || i * NT + wave * 64 < VSLOTS)  // wave-uniform
-        ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
+      {
+        if constexpr (kAsmLoads)
+          ld_lds16_asm(vwords, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
+        else
+          ld_buf_lds(vrsrc, Vs[buf] + (i * NT + wave * 64) * 8, vgo[i], tile);
+      }
     }
   };
   auto landed = [&]() { lds_loads_landed(); };
