@@ -102,10 +102,12 @@ template <int D> __device__ __forceinline__ int tile_offset(int sl, int64_t row_
   return 4 * c < dr ? (row * (int)row_stride + 4 * c) * (int)sizeof(float) : (int)kPadOffset;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int rows, int64_t row_stride, int dr) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0,
-                                           (int)(((int64_t)(rows - 1) * row_stride + dr) * (int)sizeof(float)),
-                                           0x00020000);
+// The tiles are staged with the inline-assembly direct loads (ld_lds16_asm):
+// the compiler would otherwise wait for a step's prefetch into the other stage
+// before the step's first fragment read. Each step still waits for all its
+// loads before its closing barrier.
+__device__ __forceinline__ rsrc_words rows_rsrc(const float* base, int rows, int64_t row_stride, int dr) {
+  return make_rsrc_words(base, (int)(((int64_t)(rows - 1) * row_stride + dr) * (int)sizeof(float)));
 }
 
 // dq kernel: one block = 4 waves x 32 query rows over one (sequence, kv head),
@@ -198,8 +200,8 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
 
   const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
-  const __amdgpu_buffer_rsrc_t krs = rows_rsrc(kbase, S, a.ks[1], a.dr);
-  const __amdgpu_buffer_rsrc_t vrs = rows_rsrc(vbase, S, a.vs[1], a.dr);
+  const rsrc_words krs = rows_rsrc(kbase, S, a.ks[1], a.dr);
+  const rsrc_words vrs = rows_rsrc(vbase, S, a.vs[1], a.dr);
   int kgo[TI], vgo[TI];
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
@@ -210,8 +212,8 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
       const int at = (i * kF32DqThreads + wave * 64) * 4;
-      ld_buf_lds(krs, &KV[buf][at], kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(float));
-      ld_buf_lds(vrs, &KV[buf][TILE + at], vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(float));
+      ld_lds16_asm(krs, &KV[buf][at], kgo[i], t * BN * (int)a.ks[1] * (int)sizeof(float));
+      ld_lds16_asm(vrs, &KV[buf][TILE + at], vgo[i], t * BN * (int)a.vs[1] * (int)sizeof(float));
     }
   };
 
@@ -222,6 +224,7 @@ void attn_bwd_f32_dq_kernel(BwdArgs a) {
     for (int r = 0; r < 16; ++r) dq[dt][r] = 0.f;
   const float c = a.c;
 
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), seen by the compiler: its own loads are done
   issue(0, 0);
   lds_loads_landed();
   __syncthreads();
@@ -371,17 +374,16 @@ void attn_bwd_f32_dkdv_kernel(BwdArgs a) {
     const int r0 = (u0 + it % n_u) * BQ;
     const float* qb = static_cast<const float*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const float* gb = static_cast<const float*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
-    const __amdgpu_buffer_rsrc_t qrs = rows_rsrc(qb, S, a.qs[1], a.dr);
-    const __amdgpu_buffer_rsrc_t grs = rows_rsrc(gb, S, a.gs[1], a.dr);
+    const rsrc_words qrs = rows_rsrc(qb, S, a.qs[1], a.dr);
+    const rsrc_words grs = rows_rsrc(gb, S, a.gs[1], a.dr);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
-      ld_buf_lds(i < TI / 2 ? qrs : grs, &QG[st][(i * kF32DkdvThreads + wave * 64) * 4], go[i],
+      ld_lds16_asm(i < TI / 2 ? qrs : grs, &QG[st][(i * kF32DkdvThreads + wave * 64) * 4], go[i],
                  r0 * (int)(i < TI / 2 ? a.qs[1] : a.gs[1]) * (int)sizeof(float));
     if (wave < 2) {
       const float* rb = a.dsum + b * a.lse_bs + hq * a.lse_hs + start + (wave == 0 ? a.lse_n : 0);
-      const __amdgpu_buffer_rsrc_t rrs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)rb, (short)0, S * (int)sizeof(float), 0x00020000);
-      ld_buf_lds4(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
+      const rsrc_words rrs = make_rsrc_words(rb, S * (int)sizeof(float));
+      ld_lds4_asm(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
     }
   };
 
@@ -391,6 +393,7 @@ void attn_bwd_f32_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
 
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), seen by the compiler: its own loads are done
   issue(0, 0);
   lds_loads_landed();
   __syncthreads();
@@ -568,17 +571,16 @@ void attn_bwd_f32_dkdv_wide_kernel(BwdArgs a) {
     const int r0 = (u0 + it % n_u) * BQ;
     const float* qb = static_cast<const float*>(a.q) + b * a.qs[0] + hq * a.qs[2] + start * a.qs[1];
     const float* gb = static_cast<const float*>(a.dout) + b * a.gs[0] + hq * a.gs[2] + start * a.gs[1];
-    const __amdgpu_buffer_rsrc_t qrs = rows_rsrc(qb, S, a.qs[1], a.dr);
-    const __amdgpu_buffer_rsrc_t grs = rows_rsrc(gb, S, a.gs[1], a.dr);
+    const rsrc_words qrs = rows_rsrc(qb, S, a.qs[1], a.dr);
+    const rsrc_words grs = rows_rsrc(gb, S, a.gs[1], a.dr);
 #pragma unroll
     for (int i = 0; i < TI; ++i)
-      ld_buf_lds(i < TI / 2 ? qrs : grs, &QG[st][(i * kF32DqThreads + wave * 64) * 4], go[i],
+      ld_lds16_asm(i < TI / 2 ? qrs : grs, &QG[st][(i * kF32DqThreads + wave * 64) * 4], go[i],
                  r0 * (int)(i < TI / 2 ? a.qs[1] : a.gs[1]) * (int)sizeof(float));
     if (wave < 2) {
       const float* rb = a.dsum + b * a.lse_bs + hq * a.lse_hs + start + (wave == 0 ? a.lse_n : 0);
-      const __amdgpu_buffer_rsrc_t rrs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)rb, (short)0, S * (int)sizeof(float), 0x00020000);
-      ld_buf_lds4(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
+      const rsrc_words rrs = make_rsrc_words(rb, S * (int)sizeof(float));
+      ld_lds4_asm(rrs, RV[st][wave], lane * (int)sizeof(float), r0 * (int)sizeof(float));
     }
   };
 
@@ -588,6 +590,7 @@ void attn_bwd_f32_dkdv_wide_kernel(BwdArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc_v[dt][r] = acc_k[dt][r] = 0.f;
 
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), seen by the compiler: its own loads are done
   issue(0, 0);
   lds_loads_landed();
   __syncthreads();

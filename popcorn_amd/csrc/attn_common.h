@@ -70,8 +70,9 @@ __device__ __forceinline__ rsrc_words make_rsrc_words(const void* base, int nrec
 // read what it wrote. It must also let the compiler finish its own vector
 // loads before issuing these: its waits count loads by number, and loads it
 // does not know of would make them wait for more than they mean to.
+// (A generic pointer into LDS holds the LDS address in its low 32 bits.)
 __device__ __forceinline__ uint32_t lds_base(const void* lds) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
 }
 __device__ __forceinline__ void ld_lds16_asm(rsrc_words r, const void* lds, int voffset, int soffset) {
   asm volatile("buffer_load_dwordx4 %1, %2, %3 offen lds" ::"{m0}"(lds_base(lds)), "v"(voffset), "s"(r),
