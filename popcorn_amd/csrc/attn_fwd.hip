@@ -191,11 +191,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
-  // 192-dim rows stage their tiles through the inline-assembly loads, so the
-  // step's fragment reads do not first wait for the step's own prefetch (each
-  // step waits for all its loads before its closing barrier). Measured slower
-  // at 128 dims, and at 256 the extra registers spill.
-  constexpr bool kAsmLoads = D == 192;
+  // 192- and 256-dim rows stage their tiles through the inline-assembly loads,
+  // so the step's fragment reads do not first wait for the step's own prefetch
+  // (each step waits for all its loads before its closing barrier). Measured
+  // slower at 128 dims.
+  constexpr bool kAsmLoads = D >= 192;
   const rsrc_words kwords = make_rsrc_words(kbase, k_bytes), vwords = make_rsrc_words(vbase, v_bytes);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
@@ -211,10 +211,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
     raw.w ^= a.q_flip;
     qf[kk] = __builtin_bit_cast(Frag, raw);
   }
-  if constexpr (kAsmLoads) {  // the compiler's own loads complete before the first inline-assembly load
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) asm volatile("" ::"v"(qf[kk]));
-  }
+  // the compiler's own loads complete (a wait it sees: vmcnt(0)) before the first inline-assembly load
+  if constexpr (kAsmLoads) __builtin_amdgcn_s_waitcnt(0x0F70);
 
   const int kv_end = CAUSAL ? min(m0 + rows_per_block, S) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
