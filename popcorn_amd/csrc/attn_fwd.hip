@@ -191,11 +191,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_
   const int v_bytes = (int)(((int64_t)(S - 1) * a.vss + a.dr) * (int)sizeof(T));
   const __amdgpu_buffer_rsrc_t krsrc = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, v_bytes, 0x00020000);
-  // 192- and 256-dim rows stage their tiles through the inline-assembly loads,
-  // so the step's fragment reads do not first wait for the step's own prefetch
-  // (each step waits for all its loads before its closing barrier). Measured
-  // slower at 128 dims.
-  constexpr bool kAsmLoads = D >= 192;
+  // 32-, 96-, 192- and 256-dim rows stage their tiles through the
+  // inline-assembly loads, so the step's fragment reads do not first wait for
+  // the step's own prefetch (each step waits for all its loads before its
+  // closing barrier). Measured slower at 128 dims and no faster at 64.
+  constexpr bool kAsmLoads = D != 64 && D != 128;
   const rsrc_words kwords = make_rsrc_words(kbase, k_bytes), vwords = make_rsrc_words(vbase, v_bytes);
 
   // ---- Q^T fragments: qf[kk] = Q[q_row][16kk + 8g .. +8], sign-flipped for a negative scale
