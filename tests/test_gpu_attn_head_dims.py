@@ -92,7 +92,7 @@ def test_attn_head_dim_96_is_the_128_kernel_on_zero_padded_rows():
         assert torch.equal(b_[..., d:], torch.zeros_like(b_[..., d:]))
 
 
-@pytest.mark.parametrize("d", [32, 96, 256])
+@pytest.mark.parametrize("d", [16, 32, 80, 96, 192, 256])
 def test_attn_varlen_head_dims(d):
     total, hq, hkv = 300, 8, 2
     cu = R.cuts(torch.zeros(4, dtype=torch.int64), {"total": total}, torch.Generator().manual_seed(d))
